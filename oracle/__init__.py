@@ -1,0 +1,287 @@
+"""CPU oracle for the fgm-kernels quantized-matmul path -- TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker; the product library
+(``fastgemma_amd``) never touches it.
+
+Two CPU implementations are reachable from here:
+
+* ``liboracle.so`` -- ``fgm_oracle.c``, a scalar C restatement of the reference
+  algorithm (file:line citations in that file), plus the pthread pool in
+  ``cpu_pool.c`` that reproduces the reference's N-split.
+* ``_ref/libfgmref.so`` / ``_ref/libfgmref_amx.so`` -- the reference's own
+  ``vnni_gemm.c`` + ``ops.c`` / ``amx_gemm.c`` compiled from their sources by
+  ``oracle/Makefile`` (built only where ``/root/reference`` exists; the built
+  files travel with the tree).  ``ref()`` / ``ref_amx()`` return ``None`` when a
+  library is missing or the host CPU lacks the ISA it needs.
+
+Pinning status of each oracle function is listed in ``__all__``'s functions'
+docstrings and checked by ``tests/test_oracle.py``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+_REF_AMX = None
+
+_i = C.c_int
+_p = C.c_void_p
+_u64 = C.c_uint64
+_sz = C.c_size_t
+_f = C.c_float
+
+
+def _build_oracle() -> None:
+    subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
+
+
+def lib() -> C.CDLL:
+    """The oracle library (built on first use if absent)."""
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            _build_oracle()
+        L = C.CDLL(path)
+        L.orc_f16_to_f32.restype = _f
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [_f]
+        L.orc_quant_act.argtypes = [_p, _i, _i, _p, _p]
+        L.orc_packed_a_len.restype = _sz
+        L.orc_packed_a_len.argtypes = [_i, _i]
+        L.orc_pack_a.argtypes = [_i, _i, _p, _p]
+        L.orc_fwht.argtypes = [_p, _i, _i]
+        L.orc_prep_rows.argtypes = [_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i]
+        L.orc_pack_b_tiles.argtypes = [_p, _i, _i, _p]
+        L.orc_pack_nibbles.argtypes = [_p, _sz, _p]
+        L.orc_unpack_nibbles.argtypes = [_p, _sz, _p]
+        L.orc_acc_q8c.argtypes = [_i, _i, _p, _p, _p, _i, _i, _i]
+        L.orc_gemm_q8c.argtypes = [_i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _i]
+        L.orc_acc_q4g.argtypes = [_i, _i, _p, _p, _i, _p, _i, _i, _i]
+        L.orc_gemm_q4g.argtypes = [_i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _i, _i]
+        L.orc_gen_i8.argtypes = [_u64, _sz, _i, _i, _p]
+        L.orc_gen_u8.argtypes = [_u64, _sz, _p]
+        L.orc_gen_uniform.argtypes = [_u64, _sz, _f, _f, _p]
+        L.orc_gen_normal.argtypes = [_u64, _sz, _p]
+        L.orc_gen_student_t.argtypes = [_u64, _sz, _i, _p]
+        L.orc_xorshift_fill.restype = _u64
+        L.orc_xorshift_fill.argtypes = [_u64, _sz, _i, _i, _p]
+        L.orc_lcg_fill.restype = C.c_uint32
+        L.orc_lcg_fill.argtypes = [C.c_uint32, _sz, _i, _i, _p]
+        L.orc_pool_start.restype = _i
+        L.orc_pool_start.argtypes = [_i]
+        L.orc_pool_q8c.argtypes = [_p, _i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]
+        L.orc_pool_q4g.argtypes = [_p, _i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _i, _p]
+        L.orc_pool_prep.argtypes = [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _p]
+        _LIB = L
+    return _LIB
+
+
+def _bind_ref(L: C.CDLL) -> None:
+    L.fgm_cpu_has_amx.restype = _i
+    L.fgm_cpu_has_avx512_vnni.restype = _i
+    for name in ("fgm_gemm_q8c_vnni",):
+        getattr(L, name).argtypes = [_i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _i]
+    L.fgm_gemm_q4g_vnni.argtypes = [_i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _i, _i]
+    L.fgm_quant_act.argtypes = [_p, _i, _i, _p, _p]
+    L.fgm_pack_a.argtypes = [_i, _i, _p, _p]
+    L.fgm_fwht.argtypes = [_p, _i, _i]
+    L.fgm_prep_rows.argtypes = [_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i]
+
+
+def ref() -> C.CDLL | None:
+    """The reference's own VNNI path (vnni_gemm.c + ops.c), or None."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(HERE, "_ref", "libfgmref.so")
+        if not os.path.exists(path):
+            return None
+        L = C.CDLL(path)
+        _bind_ref(L)
+        if not L.fgm_cpu_has_avx512_vnni():
+            return None
+        _REF = L
+    return _REF
+
+
+def ref_amx() -> C.CDLL | None:
+    """The reference's own AMX path (amx_gemm.c), or None (no file / no AMX)."""
+    global _REF_AMX
+    if _REF_AMX is None:
+        r = ref()
+        path = os.path.join(HERE, "_ref", "libfgmref_amx.so")
+        if r is None or not r.fgm_cpu_has_amx() or not os.path.exists(path):
+            return None
+        L = C.CDLL(path)
+        L.fgm_amx_init.restype = _i
+        L.fgm_gemm_q8c.argtypes = [_i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _i]
+        L.fgm_gemm_q4g.argtypes = [_i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _i, _i]
+        if not L.fgm_amx_init():
+            return None
+        _REF_AMX = L
+    return _REF_AMX
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+# --------------------------------------------------------------- generators
+def gen_i8(seed: int, n: int, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(n, np.int8)
+    lib().orc_gen_i8(seed, n, lo, hi, _ptr(out))
+    return out
+
+
+def gen_u8(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint8)
+    lib().orc_gen_u8(seed, n, _ptr(out))
+    return out
+
+
+def gen_uniform(seed: int, n: int, lo: float, hi: float) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_gen_uniform(seed, n, lo, hi, _ptr(out))
+    return out
+
+
+def gen_normal(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_gen_normal(seed, n, _ptr(out))
+    return out
+
+
+def gen_student_t(seed: int, n: int, nu: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_gen_student_t(seed, n, nu, _ptr(out))
+    return out
+
+
+class XorShift:
+    """vnni_test.c:39-43's generator with its running state."""
+
+    def __init__(self, state: int = 0x243F6A8885A308D3):
+        self.s = state
+
+    def ints(self, n: int, lo: int, hi: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        self.s = lib().orc_xorshift_fill(self.s, n, lo, hi, _ptr(out))
+        return out
+
+
+class Lcg:
+    """gemm_test.c:30-31's generator with its running state."""
+
+    def __init__(self, state: int = 12345):
+        self.s = state
+
+    def ints(self, n: int, lo: int, hi: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        self.s = lib().orc_lcg_fill(self.s, n, lo, hi, _ptr(out))
+        return out
+
+
+# ------------------------------------------------------------------ helpers
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    L = lib()
+    h = np.ascontiguousarray(h, np.uint16)
+    return np.array([L.orc_f16_to_f32(int(v)) for v in h.ravel()], np.float32).reshape(h.shape)
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    x = np.ascontiguousarray(x, np.float32)
+    return np.array([L.orc_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def packed_a_len(m: int, k: int) -> int:
+    return (m + 15) // 16 * 16 * k
+
+
+# ----------------------------------------------------------------- the path
+def quant_act(x: np.ndarray, rows: int, k: int):
+    """fgm_quant_act (ops.c:181-204) -> (q int8 [rows, k], scale f32 [rows])."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty((rows, k), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().orc_quant_act(_ptr(x), rows, k, _ptr(q), _ptr(s))
+    return q, s
+
+
+def pack_a(m: int, k: int, a: np.ndarray) -> np.ndarray:
+    """fgm_pack_a (ops.c:279-290)."""
+    a = np.ascontiguousarray(a, np.int8)
+    ap = np.empty(packed_a_len(m, k), np.int8)
+    lib().orc_pack_a(m, k, _ptr(a), _ptr(ap))
+    return ap
+
+
+def fwht(x: np.ndarray, hsz: int) -> np.ndarray:
+    """fgm_fwht (ops.c:153-175), returns a rotated copy."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    lib().orc_fwht(_ptr(y), y.size, hsz)
+    return y
+
+
+def prep_rows(src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1) -> None:
+    """fgm_prep_rows (ops.c:293-314), in place on caller buffers."""
+    lib().orc_prep_rows(_ptr(src), lda, _ptr(rot), _ptr(qa), _ptr(qs), _ptr(pa),
+                        m, k, hsz, r0, r1)
+
+
+def pack_b_tiles(q: np.ndarray) -> np.ndarray:
+    """pack_b_tiles (quant.py:96-107): q [N, K] int8 -> VNNI tile stream."""
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    out = np.empty(n * k, np.int8)
+    lib().orc_pack_b_tiles(_ptr(q), n, k, _ptr(out))
+    return out
+
+
+def pack_nibbles(flat: np.ndarray) -> np.ndarray:
+    """pack_nibbles (quant.py:76-82)."""
+    flat = np.ascontiguousarray(flat, np.int8)
+    out = np.empty(flat.size // 2, np.uint8)
+    lib().orc_pack_nibbles(_ptr(flat), flat.size, _ptr(out))
+    return out
+
+
+def unpack_nibbles(packed: np.ndarray) -> np.ndarray:
+    """unpack_nibbles (quant.py:85-92)."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    out = np.empty(packed.size * 2, np.int8)
+    lib().orc_unpack_nibbles(_ptr(packed), out.size, _ptr(out))
+    return out
+
+
+def acc_q8c(m, k, ap, b, n0, n1, ldacc):
+    acc = np.zeros((m, ldacc), np.int32)
+    lib().orc_acc_q8c(m, k, _ptr(ap), _ptr(b), _ptr(acc), ldacc, n0, n1)
+    return acc
+
+
+def acc_q4g(m, k, ap, bq, group, n0, n1, ldacc):
+    acc = np.zeros((k // group, m, ldacc), np.int32)
+    lib().orc_acc_q4g(m, k, _ptr(ap), _ptr(bq), group, _ptr(acc), ldacc, n0, n1)
+    return acc
+
+
+def gemm_q8c(m, n, k, ap, a_scale, b, b_scale, c, ldc, n0, n1) -> None:
+    """fgm_gemm_q8c_vnni (vnni_gemm.c:224-245), in place on c."""
+    lib().orc_gemm_q8c(m, n, k, _ptr(ap), _ptr(a_scale), _ptr(b), _ptr(b_scale), _ptr(c),
+                       ldc, n0, n1)
+
+
+def gemm_q4g(m, n, k, ap, a_scale, bq, b_scale, group, c, ldc, n0, n1) -> None:
+    """fgm_gemm_q4g_vnni (vnni_gemm.c:291-322), in place on c."""
+    lib().orc_gemm_q4g(m, n, k, _ptr(ap), _ptr(a_scale), _ptr(bq), _ptr(b_scale), group,
+                       _ptr(c), ldc, n0, n1)

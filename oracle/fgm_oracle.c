@@ -1,0 +1,414 @@
+/*
+ * fgm_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain scalar C restatement of fastgemma's fgm-kernels quantized-matmul
+ * path, written from the reference's algorithm so that the HIP kernels in
+ * fastgemma_amd/csrc can be checked against it.  Nothing in the product
+ * library links, loads or calls this file; only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may use it, and only as the checker.
+ *
+ * Every function names the reference file:line it restates (paths relative to
+ * the fastgemma repository root).  The floating-point operations are written
+ * in exactly the reference's order, so the oracle is bit-exact with the
+ * reference's VNNI / AMX kernels on finite inputs:
+ *
+ *   quant_act  : s = (amax == 0) ? 1 : amax / 127;  inv = 1 / s;
+ *                q = sat_i8(cvt_rne(x * inv))                 ops.c:181-204
+ *   gemm_q8c   : C = (float)acc * (b_scale[n] * a_scale[m])   vnni_gemm.c:208-219
+ *   gemm_q4g   : C = 0; per group g ascending:
+ *                C = fmaf((float)acc_g, f16(b_scale[g][n]), C);
+ *                then C *= a_scale[m]                         vnni_gemm.c:258-285,316-321
+ *   fwht       : butterflies len = 1, 2, 4 ... then x *= 1/sqrt(hsz)
+ *                (the final scale is skipped when hsz < 16)   ops.c:153-175
+ *
+ * Pinning (what checks each function beyond "same formula twice"): see
+ * tests/test_oracle.py -- the reference's own known-answer nibble table,
+ * closed forms, brute-force int64 sums through an independent layout decode,
+ * M-invariance / n-range invariance, and byte-for-byte comparison against the
+ * reference's own C compiled from its sources into oracle/_ref.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------ f16 helpers */
+
+/* Exact IEEE binary16 -> binary32 widening (every half value is exactly
+ * representable in single precision).  The reference widens with
+ * _mm512_cvtph_ps / _cvtsh_ss (vnni_gemm.c:272-275, vnni_test.c:112). */
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1F;
+  uint32_t man = h & 0x3FF;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else { /* subnormal half: normalise */
+      int e = -1;
+      do { man <<= 1; e++; } while (!(man & 0x400));
+      man &= 0x3FF;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 0x1F) {
+    bits = sign | 0x7F800000u | (man << 13);
+  } else {
+    bits = sign | ((exp - 15 + 127) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* binary32 -> binary16, round to nearest even (what numpy's astype(float16)
+ * and _cvtss_sh(x, 0) do).  Used only to make synthetic f16 group scales,
+ * the way the converter stores them (quant.py:165). */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000;
+  uint32_t exp = (x >> 23) & 0xFF;
+  uint32_t man = x & 0x7FFFFF;
+  if (exp == 0xFF) return (uint16_t)(sign | 0x7C00 | (man ? 0x200 | (man >> 13) : 0));
+  int e = (int)exp - 127 + 15;
+  if (e >= 0x1F) return (uint16_t)(sign | 0x7C00);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    man |= 0x800000;
+    int shift = 14 - e;
+    uint32_t half = man >> shift;
+    uint32_t rem = man & ((1u << shift) - 1);
+    uint32_t mid = 1u << (shift - 1);
+    if (rem > mid || (rem == mid && (half & 1))) half++;
+    return (uint16_t)(sign | half);
+  }
+  uint32_t half = ((uint32_t)e << 10) | (man >> 13);
+  uint32_t rem = man & 0x1FFF;
+  if (rem > 0x1000 || (rem == 0x1000 && (half & 1))) half++;
+  return (uint16_t)(sign | half);
+}
+
+/* ------------------------------------------------ activation quantisation */
+
+/* _mm512_cvtps_epi32 under the default MXCSR (round to nearest even): a NaN or
+ * an out-of-range value gives the "integer indefinite" 0x80000000. */
+static int32_t cvt_ps_epi32_rne(float v) {
+  if (!(fabsf(v) < 2147483648.0f)) return INT32_MIN;
+  return (int32_t)rintf(v);
+}
+
+/* _mm512_cvtsepi32_epi8: signed saturation to [-128, 127]. */
+static int8_t sat_i8(int32_t v) {
+  return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v));
+}
+
+/* The scalar tail of fgm_quant_act (ops.c:199-202): (int)lrintf(v) clamped to
+ * [-127, 127].  On x86-64 lrintf is cvtss2si with a 64-bit destination (NaN or
+ * |v| >= 2^63 gives INT64_MIN), and the (int) cast keeps the low 32 bits. */
+static int8_t tail_q(float v) {
+  int64_t l;
+  if (!(fabsf(v) < 9223372036854775808.0f)) l = INT64_MIN;
+  else l = (int64_t)rintf(v);
+  int32_t iv = (int32_t)(uint32_t)(uint64_t)l;
+  return (int8_t)(iv > 127 ? 127 : (iv < -127 ? -127 : iv));
+}
+
+/* fgm_quant_act, ops.c:181-204.  Per-row symmetric int8.
+ * The reference reduces |x| with 16-lane _mm512_max_ps and a final tree; for
+ * rows without NaN the maximum is order-free, which is what this restates.
+ * (Rows containing NaN are outside the parity contract: the reference's
+ * answer then depends on which SIMD lane the NaN lands in.) */
+void orc_quant_act(const float *x, int rows, int k, int8_t *q, float *scale) {
+  const int kv = k & ~15; /* elements handled by the 16-wide vector loop */
+  for (int r = 0; r < rows; r++) {
+    const float *src = x + (size_t)r * k;
+    float m = 0.0f;
+    for (int i = 0; i < k; i++) {
+      float a = fabsf(src[i]);
+      if (a > m) m = a;
+    }
+    float s = (m == 0.0f) ? 1.0f : m / 127.0f;
+    float inv = 1.0f / s;
+    scale[r] = s;
+    int8_t *dst = q + (size_t)r * k;
+    for (int i = 0; i < kv; i++) dst[i] = sat_i8(cvt_ps_epi32_rne(src[i] * inv));
+    for (int i = kv; i < k; i++) dst[i] = tail_q(src[i] * inv);
+  }
+}
+
+/* ------------------------------------------------------------- A packing */
+
+/* packed_a_len, lib.rs:155-157. */
+size_t orc_packed_a_len(int m, int k) { return (size_t)((m + 15) / 16) * 16 * (size_t)k; }
+
+/* fgm_pack_a, ops.c:279-290: [MB][KB][16 rows][64 bytes]; rows >= M zero. */
+void orc_pack_a(int M, int K, const int8_t *A, int8_t *Ap) {
+  const int KB = K / 64, MB = (M + 15) / 16;
+  for (int mb = 0; mb < MB; mb++)
+    for (int kb = 0; kb < KB; kb++)
+      for (int r = 0; r < 16; r++) {
+        int m = mb * 16 + r;
+        int8_t *d = Ap + (((size_t)mb * KB + kb) * 16 + r) * 64;
+        for (int j = 0; j < 64; j++) d[j] = (m < M) ? A[(size_t)m * K + kb * 64 + j] : 0;
+      }
+}
+
+/* Inverse of the packing: A[m][k] out of the packed tiles. */
+static inline int8_t apk(const int8_t *Ap, int K, int m, int k) {
+  const int KB = K / 64;
+  return Ap[(((size_t)(m / 16) * KB + k / 64) * 16 + (m % 16)) * 64 + (k % 64)];
+}
+
+/* ------------------------------------------------------------------- FWHT */
+
+/* fgm_fwht, ops.c:153-175.  In place on contiguous blocks of hsz (power of 2);
+ * butterfly stages len = 1, 2, 4, ...; each stage writes (u + v, u - v).
+ * scale = 1 / sqrtf(hsz), applied 16 at a time, so hsz < 16 is not scaled. */
+void orc_fwht(float *x, int n, int hsz) {
+  const float scale = 1.0f / sqrtf((float)hsz);
+  for (int b = 0; b < n; b += hsz) {
+    float *p = x + b;
+    for (int len = 1; len < hsz; len <<= 1)
+      for (int i = 0; i < hsz; i += len << 1)
+        for (int j = i; j < i + len; j++) {
+          float u = p[j], v = p[j + len];
+          p[j] = u + v;
+          p[j + len] = u - v;
+        }
+    for (int i = 0; i < hsz / 16 * 16; i++) p[i] = p[i] * scale;
+  }
+}
+
+/* fgm_prep_rows, ops.c:293-314: rows [r0, r1) -- strided copy into rot, FWHT
+ * when hsz > 0, quantise, then tile-pack the 16-row blocks the range covers
+ * (rows >= m of those blocks are zero-filled). */
+void orc_prep_rows(const float *src, int lda, float *rot, int8_t *qa, float *qs,
+                   int8_t *pa, int m, int k, int hsz, int r0, int r1) {
+  if (r0 >= r1) return;
+  const int n = r1 - r0;
+  for (int r = r0; r < r1; r++)
+    memcpy(rot + (size_t)r * k, src + (size_t)r * lda, (size_t)k * sizeof(float));
+  if (hsz > 0) orc_fwht(rot + (size_t)r0 * k, n * k, hsz);
+  orc_quant_act(rot + (size_t)r0 * k, n, k, qa + (size_t)r0 * k, qs + r0);
+  const int KB = k / 64;
+  for (int mb = r0 / 16; mb * 16 < r1; mb++)
+    for (int kb = 0; kb < KB; kb++)
+      for (int rr = 0; rr < 16; rr++) {
+        int row = mb * 16 + rr;
+        int8_t *d = pa + (((size_t)mb * KB + kb) * 16 + rr) * 64;
+        for (int j = 0; j < 64; j++) d[j] = (row < m) ? qa[(size_t)row * k + kb * 64 + j] : 0;
+      }
+}
+
+/* ---------------------------------------------------------- weight layout */
+
+/* Byte offset of B[k][n] in the int8 VNNI tile stream (quant.py:96-107,
+ * vnni_test.c:49-50): tiles [N/16][K/64] of 1024 bytes, each holding
+ * (K=64, N=16) as [k/4][n][k%4]. */
+static inline size_t b8_off(int K, int k, int n) {
+  const int KB = K / 64;
+  return ((size_t)(n / 16) * KB + k / 64) * 1024 + ((k % 64) / 4) * 64 + (n % 16) * 4 + k % 4;
+}
+
+/* Signed int4 B[k][n] out of the packed stream: the int8 stream above, each
+ * 64-byte block nibble-packed as packed[i] = q[i] | q[i+32] << 4
+ * (quant.py:76-82), two's-complement nibbles (vnni_test.c:52-69). */
+static inline int b4_val(const uint8_t *Bq, int K, int k, int n) {
+  size_t p = b8_off(K, k, n);
+  size_t blk = p / 64, off = p % 64;
+  uint8_t byte = Bq[blk * 32 + off % 32];
+  int v = (off < 32) ? (byte & 0xF) : (byte >> 4);
+  return (v ^ 8) - 8;
+}
+
+/* pack_b_tiles, quant.py:96-107: q[N][K] row-major (out, in) -> tile stream. */
+void orc_pack_b_tiles(const int8_t *q, int N, int K, int8_t *blob) {
+  for (int n = 0; n < N; n++)
+    for (int k = 0; k < K; k++) blob[b8_off(K, k, n)] = q[(size_t)n * K + k];
+}
+
+/* pack_nibbles, quant.py:76-82: per 64-byte block, low nibble = value i,
+ * high nibble = value i + 32. */
+void orc_pack_nibbles(const int8_t *flat, size_t nbytes, uint8_t *packed) {
+  for (size_t b = 0; b < nbytes / 64; b++)
+    for (int i = 0; i < 32; i++)
+      packed[b * 32 + i] =
+          (uint8_t)((flat[b * 64 + i] & 0xF) | ((flat[b * 64 + 32 + i] & 0xF) << 4));
+}
+
+/* unpack_nibbles, quant.py:85-92. */
+void orc_unpack_nibbles(const uint8_t *packed, size_t nbytes_out, int8_t *flat) {
+  for (size_t b = 0; b < nbytes_out / 64; b++)
+    for (int i = 0; i < 32; i++) {
+      int lo = packed[b * 32 + i] & 0xF, hi = packed[b * 32 + i] >> 4;
+      flat[b * 64 + i] = (int8_t)((lo ^ 8) - 8);
+      flat[b * 64 + 32 + i] = (int8_t)((hi ^ 8) - 8);
+    }
+}
+
+/* ------------------------------------------------------------------ GEMMs */
+
+/* Exact integer dot products, int32 wrap-around semantics (vpdpbusd does not
+ * saturate, so the reference's biased sum minus 128*asum equals the true sum
+ * modulo 2^32). */
+
+/* Raw int32 accumulators of the q8c GEMM: acc[m][n] = sum_k A[m][k] * B[k][n]
+ * for m < M, n in [16*n0, 16*n1), stored at acc[m * ldacc + n]. */
+void orc_acc_q8c(int M, int K, const int8_t *Ap, const int8_t *B, int32_t *acc, int ldacc,
+                 int n0, int n1) {
+  for (int m = 0; m < M; m++)
+    for (int n = n0 * 16; n < n1 * 16; n++) {
+      uint32_t s = 0;
+      for (int k = 0; k < K; k++)
+        s += (uint32_t)((int32_t)apk(Ap, K, m, k) * (int32_t)B[b8_off(K, k, n)]);
+      acc[(size_t)m * ldacc + n] = (int32_t)s;
+    }
+}
+
+/* fgm_gemm_q8c_vnni, vnni_gemm.c:224-245 (+ q8c_block :190-222).
+ * Writes C[m][n] for m < M, n in [16*n0, 16*n1); nothing else is touched. */
+void orc_gemm_q8c(int M, int N, int K, const int8_t *Ap, const float *a_scale,
+                  const int8_t *B, const float *b_scale, float *C, int ldc, int n0, int n1) {
+  (void)N;
+  for (int m = 0; m < M; m++)
+    for (int n = n0 * 16; n < n1 * 16; n++) {
+      uint32_t s = 0;
+      for (int k = 0; k < K; k++)
+        s += (uint32_t)((int32_t)apk(Ap, K, m, k) * (int32_t)B[b8_off(K, k, n)]);
+      float f = (float)(int32_t)s;
+      float sc = b_scale[n] * a_scale[m];
+      C[(size_t)m * ldc + n] = f * sc;
+    }
+}
+
+/* Raw per-group int32 accumulators of the q4g GEMM:
+ * acc[(g * M + m) * ldacc + n] = sum_{k in group g} A[m][k] * B[k][n]. */
+void orc_acc_q4g(int M, int K, const int8_t *Ap, const uint8_t *Bq, int group, int32_t *acc,
+                 int ldacc, int n0, int n1) {
+  const int NG = K / group;
+  for (int g = 0; g < NG; g++)
+    for (int m = 0; m < M; m++)
+      for (int n = n0 * 16; n < n1 * 16; n++) {
+        uint32_t s = 0;
+        for (int k = g * group; k < (g + 1) * group; k++)
+          s += (uint32_t)((int32_t)apk(Ap, K, m, k) * b4_val(Bq, K, k, n));
+        acc[((size_t)g * M + m) * ldacc + n] = (int32_t)s;
+      }
+}
+
+/* fgm_gemm_q4g_vnni, vnni_gemm.c:291-322 (+ q4g_block :252-289).
+ * b_scale is f16 [K/group][N]. */
+void orc_gemm_q4g(int M, int N, int K, const int8_t *Ap, const float *a_scale,
+                  const uint8_t *Bq, const uint16_t *b_scale, int group, float *C, int ldc,
+                  int n0, int n1) {
+  const int NG = K / group;
+  for (int m = 0; m < M; m++)
+    for (int n = n0 * 16; n < n1 * 16; n++) {
+      float c = 0.0f;
+      for (int g = 0; g < NG; g++) {
+        uint32_t s = 0;
+        for (int k = g * group; k < (g + 1) * group; k++)
+          s += (uint32_t)((int32_t)apk(Ap, K, m, k) * b4_val(Bq, K, k, n));
+        c = fmaf((float)(int32_t)s, orc_f16_to_f32(b_scale[(size_t)g * N + n]), c);
+      }
+      C[(size_t)m * ldc + n] = c;
+    }
+  for (int m = 0; m < M; m++)
+    for (int n = n0 * 16; n < n1 * 16; n++)
+      C[(size_t)m * ldc + n] = C[(size_t)m * ldc + n] * a_scale[m];
+}
+
+/* ------------------------------------------------------------ generators */
+
+/* The reference tests' own generators, so their case lists can be replayed
+ * with identical inputs.
+ * vnni_test.c:39-43: xorshift64 (13, 7, 17), rnd(lo, hi) = lo + s % (hi-lo+1).
+ * Returns the advanced state (the reference keeps it in one static). */
+uint64_t orc_xorshift_fill(uint64_t s, size_t n, int lo, int hi, int32_t *out) {
+  uint64_t span = (uint64_t)(hi - lo + 1);
+  for (size_t i = 0; i < n; i++) {
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    out[i] = lo + (int)(s % span);
+  }
+  return s;
+}
+
+/* gemm_test.c:30-31 and dbg.c:33-34: 32-bit LCG, value = lo + (s >> 16) % span. */
+uint32_t orc_lcg_fill(uint32_t s, size_t n, int lo, int hi, int32_t *out) {
+  uint32_t span = (uint32_t)(hi - lo + 1);
+  for (size_t i = 0; i < n; i++) {
+    s = s * 1103515245u + 12345u;
+    out[i] = lo + (int)((s >> 16) % span);
+  }
+  return s;
+}
+
+/* SplitMix64 (Steele, Lea, Flood 2014): the synthetic-input generator shared
+ * by tests and bench so both sides see identical inputs for a seed. */
+static inline uint64_t splitmix64(uint64_t *s) {
+  uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+/* Uniform integers in [lo, hi] as int8 (Lemire-free modulo: the bias is
+ * below 2^-56 for these ranges). */
+void orc_gen_i8(uint64_t seed, size_t n, int lo, int hi, int8_t *out) {
+  uint64_t s = seed;
+  uint64_t span = (uint64_t)(hi - lo + 1);
+  for (size_t i = 0; i < n; i++) out[i] = (int8_t)(lo + (int)(splitmix64(&s) % span));
+}
+
+/* Uniform bytes -- a packed int4 stream of iid uniform [-8, 7] nibbles. */
+void orc_gen_u8(uint64_t seed, size_t n, uint8_t *out) {
+  uint64_t s = seed;
+  for (size_t i = 0; i < n; i++) out[i] = (uint8_t)(splitmix64(&s) >> 56);
+}
+
+static inline double u01(uint64_t *s) { return (double)(splitmix64(s) >> 11) * 0x1.0p-53; }
+
+/* Uniform floats in [lo, hi). */
+void orc_gen_uniform(uint64_t seed, size_t n, float lo, float hi, float *out) {
+  uint64_t s = seed;
+  for (size_t i = 0; i < n; i++) out[i] = (float)(lo + (hi - lo) * u01(&s));
+}
+
+/* Standard normals (Box-Muller). */
+void orc_gen_normal(uint64_t seed, size_t n, float *out) {
+  uint64_t s = seed;
+  for (size_t i = 0; i < n; i += 2) {
+    double u1 = u01(&s), u2 = u01(&s);
+    if (u1 < 1e-300) u1 = 1e-300;
+    double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586 * u2;
+    out[i] = (float)(r * cos(t));
+    if (i + 1 < n) out[i + 1] = (float)(r * sin(t));
+  }
+}
+
+/* Student-t with nu degrees of freedom: Z / sqrt(chi2_nu / nu), chi2 as a sum
+ * of nu squared normals (nu is a small integer here). */
+void orc_gen_student_t(uint64_t seed, size_t n, int nu, float *out) {
+  uint64_t s = seed;
+  if (nu < 1) nu = 1;
+  if (nu > 7) nu = 7;
+  for (size_t i = 0; i < n; i++) {
+    double z[8];
+    int need = nu + 1;
+    for (int j = 0; j < need; j += 2) {
+      double u1 = u01(&s), u2 = u01(&s);
+      if (u1 < 1e-300) u1 = 1e-300;
+      double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586 * u2;
+      z[j] = r * cos(t);
+      if (j + 1 < 8) z[j + 1] = r * sin(t);
+    }
+    double chi = 0;
+    for (int j = 1; j <= nu; j++) chi += z[j] * z[j];
+    out[i] = (float)(z[0] / sqrt(chi / nu));
+  }
+}

@@ -1,0 +1,157 @@
+"""Input builders for the golden cases.
+
+Shared by ``make_golden.py`` (which runs the reference's own C, compiled from
+its sources into ``oracle/_ref``, on these inputs and records its outputs in
+``ref_outputs.json``) and by the tests (which rebuild the same inputs and check
+the oracle and the HIP path against the recorded outputs).
+
+The GEMM case lists are the reference's own:
+
+* ``VNNI_CASES`` -- bench/kernels/vnni_test.c:271-284, inputs from its
+  xorshift64 (seed 0x243F6A8885A308D3, state carried across cases in the
+  order main() runs them, vnni_test.c:39-43,133-176).
+* ``AMX_CASE`` -- bench/kernels/gemm_test.c:84-130 (LCG seed 12345), the
+  M=40/N=64/K=256/g=64 case and its M=8 decode variant.
+* ``DBG_CASE`` -- bench/kernels/dbg.c:21-37 (LCG seed 7, a_scale = 1).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+# (kind, M, N, K, group, n0, n1) in vnni_test.c main() order.
+VNNI_CASES = [
+    ("q8c", 1, 256, 1536, 0, 0, 16),
+    ("q8c", 8, 256, 1536, 0, 0, 16),
+    ("q8c", 15, 256, 1536, 0, 0, 16),
+    ("q8c", 16, 256, 1536, 0, 0, 16),
+    ("q8c", 17, 256, 1536, 0, 0, 16),
+    ("q8c", 33, 512, 1536, 0, 4, 12),
+    ("q8c", 64, 256, 2048, 0, 0, 16),
+    ("q4g", 1, 256, 1536, 128, 0, 16),
+    ("q4g", 8, 256, 1536, 128, 0, 16),
+    ("q4g", 15, 256, 1536, 64, 0, 16),
+    ("q4g", 16, 256, 1536, 256, 0, 16),
+    ("q4g", 17, 256, 1536, 128, 0, 16),
+    ("q4g", 33, 512, 1536, 128, 4, 12),
+    ("q4g", 64, 256, 2048, 128, 0, 16),
+]
+
+
+def _f32(x) -> np.float32:
+    return np.float32(x)
+
+
+def vnni_inputs():
+    """Yield (case, inputs) for VNNI_CASES with vnni_test.c's exact inputs.
+
+    inputs = dict(A int8 [M, K], Ap packed, as f32 [M], B (int8 tiles or
+    packed int4 bytes), bs (f32 [N] or f16 bits [K/g, N])).
+    """
+    rs = oracle.XorShift()
+    for case in VNNI_CASES:
+        kind, M, N, K, group, n0, n1 = case
+        KB, NB = K // 64, N // 16
+        A = rs.ints(M * K, -127, 127).astype(np.int8).reshape(M, K)
+        # as[i] = 0.01f + 0.001f * (i % 7)
+        a_s = np.array([_f32(0.01) + _f32(0.001) * _f32(i % 7) for i in range(M)], np.float32)
+        if kind == "q8c":
+            B = rs.ints(NB * KB * 1024, -127, 127).astype(np.int8)
+            bs = np.array([_f32(0.02) + _f32(0.0005) * _f32(i % 11) for i in range(N)],
+                          np.float32)
+        else:
+            B = rs.ints(NB * KB * 512, 0, 255).astype(np.uint8)
+            NG = K // group
+            bsf = np.array([_f32(0.002) + _f32(0.0001) * _f32(i % 13) for i in range(NG * N)],
+                           np.float32)
+            bs = bsf.astype(np.float16).view(np.uint16).reshape(NG, N)
+        yield case, dict(A=A, Ap=oracle.pack_a(M, K, A), a_s=a_s, B=B, bs=bs)
+
+
+def amx_inputs():
+    """gemm_test.c:84-107's inputs (LCG seed 12345)."""
+    M, N, K, group = 40, 64, 256, 64
+    KB, NB = K // 64, N // 16
+    g = oracle.Lcg(12345)
+    A = g.ints(M * K, -127, 127).astype(np.int8).reshape(M, K)
+    a_s = np.array([_f32(0.002) + _f32(0.001) * _f32(i % 7) for i in range(M)], np.float32)
+    Bq = np.empty(NB * KB * 512, np.uint8)
+    for i in range(Bq.size):  # lo first, then hi (gemm_test.c:98-101)
+        lo = int(g.ints(1, -8, 7)[0]) & 0xF
+        hi = int(g.ints(1, -8, 7)[0]) & 0xF
+        Bq[i] = lo | (hi << 4)
+    B8 = g.ints(NB * KB * 1024, -127, 127).astype(np.int8)
+    bs4f = np.array([_f32(0.01) + _f32(0.001) * _f32(i % 5) for i in range((K // group) * N)],
+                    np.float32)
+    bs4 = bs4f.astype(np.float16).view(np.uint16).reshape(K // group, N)
+    bs8 = np.array([_f32(0.003) + _f32(0.0005) * _f32(i % 11) for i in range(N)], np.float32)
+    return dict(M=M, N=N, K=K, group=group, A=A, a_s=a_s, Bq=Bq, B8=B8, bs4=bs4, bs8=bs8)
+
+
+def dbg_inputs():
+    """dbg.c:23-37's inputs (LCG seed 7; a_scale = 1)."""
+    M, N, K, group = 2, 64, 128, 64
+    KB, NB = K // 64, N // 16
+    g = oracle.Lcg(7)
+    A = (g.ints(M * K, 0, 8) - 4).astype(np.int8).reshape(M, K)
+    Bq = g.ints(NB * KB * 512, 0, 255).astype(np.uint8)
+    bsf = np.array([1.0 + 0.25 * (i % 3) for i in range((K // group) * N)], np.float32)
+    bs = bsf.astype(np.float16).view(np.uint16).reshape(K // group, N)
+    return dict(M=M, N=N, K=K, group=group, A=A, a_s=np.ones(M, np.float32), Bq=Bq, bs=bs)
+
+
+def layout_inputs():
+    """Small q [N, K] matrices packed by the oracle's pack_b_tiles/pack_nibbles;
+    the reference kernel run on them with unit scales gives exact integer
+    products, pinning the packers to the reference kernel's layout."""
+    M, N, K = 5, 64, 192
+    A = oracle.gen_i8(31, M * K, -127, 127).reshape(M, K)
+    Q8 = oracle.gen_i8(32, N * K, -127, 127).reshape(N, K)
+    Q4 = oracle.gen_i8(33, N * K, -8, 7).reshape(N, K)
+    return dict(M=M, N=N, K=K, A=A, Q8=Q8, Q4=Q4)
+
+
+def quant_rows():
+    """Activation rows for quant_act / prep_rows goldens: normal, heavy-tailed,
+    outlier channels, all-zero, one non-zero, exact .5 ties, +-inf, subnormal
+    rows, and a row length that is not a multiple of 16 (the scalar tail)."""
+    K = 256
+    rows = []
+    rows.append(oracle.gen_normal(11, K))
+    rows.append(oracle.gen_student_t(12, K, 3))
+    r = oracle.gen_normal(13, K)
+    r[[5, 77]] *= 20.0
+    rows.append(r)
+    rows.append(np.zeros(K, np.float32))
+    r = np.zeros(K, np.float32)
+    r[42] = -3.5
+    rows.append(r)
+    # amax = 127 -> s = 1, inv = 1: x*inv = x, so k + 0.5 values are exact ties
+    r = np.array([(i % 40) - 20 + 0.5 for i in range(K)], np.float32)
+    r[0] = 127.0
+    rows.append(r)
+    r = oracle.gen_normal(14, K)
+    r[9] = np.inf
+    r[200] = -np.inf
+    rows.append(r)
+    rows.append((oracle.gen_normal(15, K) * np.float32(1e-39)).astype(np.float32))
+    rows.append((oracle.gen_normal(16, K) * np.float32(1e-44)).astype(np.float32))
+    rows.append((oracle.gen_normal(17, K) * np.float32(5e37)).astype(np.float32))
+    x = np.stack(rows).astype(np.float32)
+    tail = oracle.gen_normal(18, 3 * 100).reshape(3, 100)
+    tail[1, 97] = 50.0
+    tail[2, 99] = np.inf
+    return x, tail.astype(np.float32)
+
+
+def fwht_input(hsz: int) -> np.ndarray:
+    return oracle.gen_normal(100 + hsz, 4 * 256).reshape(4, 256)
+
+
+def prep_input():
+    """m=37 rows of k=256 in an lda=300 buffer."""
+    m, k, lda = 37, 256, 300
+    src = oracle.gen_normal(21, m * lda).reshape(m, lda)
+    src[3, 10] = 40.0
+    return m, k, lda, src.astype(np.float32)
