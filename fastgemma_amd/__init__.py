@@ -1,0 +1,81 @@
+"""fastgemma_amd -- MI355X (gfx950) implementation of fastgemma's fgm-kernels
+quantized-matmul path.
+
+The product is the C-ABI library ``libfgm_hip.so`` (declared in
+``include/fgm_hip.h``); this package loads it and mirrors, in Python, the
+reference's safe wrapper layer over that ABI (crates/fgm-kernels/src/lib.rs),
+so host code and tests can call the path with the reference's names, argument
+meaning and checks.
+
+There is no CPU fallback: if the library is missing, or no gfx950 device is
+usable when a kernel is called, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes as _C
+import os as _os
+
+HERE = _os.path.dirname(_os.path.abspath(__file__))
+LIB_PATH = _os.path.join(HERE, "libfgm_hip.so")
+_LIB = None
+
+
+class HipUnavailable(RuntimeError):
+    """The HIP library is not built or no gfx950 device is usable."""
+
+
+class FgmHipError(RuntimeError):
+    """A device-API call returned a non-zero status."""
+
+
+def lib() -> _C.CDLL:
+    """Load libfgm_hip.so (raises HipUnavailable if it was not built)."""
+    global _LIB
+    if _LIB is None:
+        if not _os.path.exists(LIB_PATH):
+            raise HipUnavailable(
+                f"{LIB_PATH} is missing: build it with `make -C fastgemma_amd/csrc` "
+                "or __graft_entry__.build()")
+        L = _C.CDLL(LIB_PATH)
+        _bind(L)
+        _LIB = L
+    return _LIB
+
+
+def _bind(L: _C.CDLL) -> None:
+    i, p, f = _C.c_int, _C.c_void_p, _C.c_float
+    L.fgm_hip_last_error.restype = _C.c_char_p
+    L.fgm_hip_available.restype = i
+    L.fgm_hip_init.argtypes = [i]
+    L.fgm_hip_gemm_path.argtypes = [i, i, i, i]
+    dev_q8c = [i, i, i, p, p, p, p, p, i, i, i, p]
+    dev_q4g = [i, i, i, p, p, p, p, i, p, i, i, i, p]
+    L.fgm_hip_gemm_q8c_dev.argtypes = dev_q8c
+    L.fgm_hip_gemm_q4g_dev.argtypes = dev_q4g
+    L.fgm_hip_acc_q8c_dev.argtypes = [i, i, i, p, p, p, i, i, i, p]
+    L.fgm_hip_acc_q4g_dev.argtypes = [i, i, i, p, p, i, p, i, i, i, p]
+    L.fgm_hip_prep_rows_dev.argtypes = [p, i, p, p, p, p, i, i, i, i, i, p]
+    L.fgm_hip_quant_act_dev.argtypes = [p, i, i, p, p, p]
+    L.fgm_hip_pack_a_dev.argtypes = [i, i, p, p, p]
+    L.fgm_hip_fwht_dev.argtypes = [p, i, i, p]
+    L.fgm_gemm_q8c_hip.argtypes = [i, i, i, p, p, p, p, p, i, i, i]
+    L.fgm_gemm_q4g_hip.argtypes = [i, i, i, p, p, p, p, i, p, i, i, i]
+    L.fgm_pack_a_hip.argtypes = [i, i, p, p]
+    L.fgm_prep_rows_hip.argtypes = [p, i, p, p, p, p, i, i, i, i, i]
+    L.fgm_quant_act_hip.argtypes = [p, i, i, p, p]
+    L.fgm_fwht_hip.argtypes = [p, i, i]
+    for name in ("fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
+                 "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
+                 "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path"):
+        getattr(L, name).restype = i
+    del f
+
+
+def check(status: int) -> None:
+    """Raise FgmHipError with the library's message for a non-zero status."""
+    if status != 0:
+        raise FgmHipError(f"status {status}: {lib().fgm_hip_last_error().decode()}")
+
+
+from .kernels import (  # noqa: E402,F401
+    Backend, backend, fwht, gemm_q4g, gemm_q8c, pack_a, packed_a_len, prep_rows, quant_act)

@@ -1,0 +1,67 @@
+// Shared device helpers for the gfx950 kernels of the fgm quantized-matmul path.
+//
+// Operand layouts (unchanged from the .fgm file, see include/fgm_hip.h):
+//   packed A   [MB][KB][16 rows][64 bytes]            (ops.c:279-290)
+//   int8 B     [N/16][K/64] tiles of 1024 bytes, each (K=64,N=16) as
+//              [k/4][n][k%4]                          (quant.py:96-107)
+//   int4 B     the int8 stream nibble-packed per 64-byte block:
+//              packed[i] = q[i] | q[i+32] << 4        (quant.py:76-82)
+//
+// MFMA mapping used by every GEMM kernel here (v_mfma_i32_16x16x64_i8):
+//   lane l = 16*g + j (g = l/16 in 0..3, j = l%16)
+//   A operand: row j, B operand: column j; operand byte 4*t + e (t, e in
+//   0..3) carries k = 16*t + 4*g + e of the 64-wide k-block.  The hardware
+//   pairs A and B bytes by (lane group, byte), so this k-permutation leaves
+//   the int32 sum exact.  With it, lane l's B bytes for t are the dword at
+//   byte 256*t + 4*l of a 1024-byte int8 tile -- each of the four loads of a
+//   wave reads 256 contiguous bytes.
+//   Output: lane l, register r holds D[4*g + r][j].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+#define FGM_DEV static __device__ __forceinline__
+
+// Signed int4 -> int8 for four nibbles at once: `x` holds four raw nibbles in
+// the low half of each byte.  ((u ^ 8) + 120) ^ 128 == (u ^ 8) - 8 per byte,
+// with no carry across bytes (the sum stays in 120..135).  Two's-complement
+// nibbles, as amx_gemm.c:80-89 and vnni_test.c:52-69 define them.
+FGM_DEV uint32_t nib4_to_i8x4(uint32_t u) {
+  return ((u ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u;
+}
+
+// Exact IEEE half -> float (v_cvt_f32_f16 is exact for every half).
+FGM_DEV float f16_bits_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;
+}
+
+FGM_DEV v4i mfma16(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Quantisation of one activation value, reproducing fgm_quant_act
+// (ops.c:195-203) bit for bit:
+//   vector part (index < k & ~15): _mm512_cvtps_epi32 (round to nearest even;
+//   NaN or |v| >= 2^31 gives 0x80000000) then _mm512_cvtsepi32_epi8
+//   (saturate to [-128, 127]);
+//   scalar tail: (int)lrintf(v) -- cvtss2si with a 64-bit result, NaN or
+//   |v| >= 2^63 gives INT64_MIN, (int) keeps the low 32 bits -- clamped to
+//   [-127, 127].
+FGM_DEV int8_t quant_vec(float v) {
+  if (!(__builtin_fabsf(v) < 2147483648.0f)) return (int8_t)-128;
+  float r = __builtin_rintf(v);
+  r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);
+  return (int8_t)(int)r;
+}
+
+FGM_DEV int8_t quant_tail(float v) {
+  int64_t l;
+  if (!(__builtin_fabsf(v) < 9223372036854775808.0f)) l = INT64_MIN;
+  else l = (int64_t)__builtin_rintf(v);
+  int32_t iv = (int32_t)(uint32_t)(uint64_t)l;
+  return (int8_t)(iv > 127 ? 127 : (iv < -127 ? -127 : iv));
+}

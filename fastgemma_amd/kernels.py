@@ -1,0 +1,183 @@
+"""Python mirror of the reference's kernel wrapper layer.
+
+Each function has the name, argument order, argument meaning and checks of
+the safe wrapper it mirrors in crates/fgm-kernels/src/lib.rs; the reference's
+``debug_assert!``s are always-on assertions here.  Buffers may be
+
+* numpy arrays (host memory): the call goes to the drop-in ``fgm_*_hip``
+  symbol, which moves A / C per call and caches weights on the GPU;
+* torch tensors on the GPU: the call goes to the device API
+  (``fgm_hip_*_dev``) on torch's current stream, asynchronously.
+
+Mixing the two in one call is an error.
+"""
+from __future__ import annotations
+
+import enum
+import os
+
+import numpy as np
+
+from . import check, lib, HipUnavailable
+
+
+class Backend(enum.Enum):
+    """Which GEMM kernel the process uses (lib.rs:84-100).  The reference's
+    Amx / Vnni CPU backends live in the reference; this library is Hip."""
+
+    Hip = "hip"
+
+    def name_str(self) -> str:
+        return "hip-gfx950"
+
+
+_BACKEND = None
+
+
+def backend() -> Backend:
+    """The backend for this process, decided once (lib.rs:112-137).
+
+    ``FGM_BACKEND=hip`` or unset selects the GPU; the reference's CPU values
+    (``amx``, ``vnni``) are refused, since those kernels are not in this
+    library.  Raises HipUnavailable without a usable gfx950 device."""
+    global _BACKEND
+    if _BACKEND is None:
+        want = os.environ.get("FGM_BACKEND", "hip")
+        if want != "hip":
+            raise HipUnavailable(f"FGM_BACKEND={want}: this library provides only the hip backend")
+        if not lib().fgm_hip_available():
+            raise HipUnavailable(lib().fgm_hip_last_error().decode() or "no gfx950 device")
+        _BACKEND = Backend.Hip
+    return _BACKEND
+
+
+# ------------------------------------------------------------------ helpers
+def _is_dev(x) -> bool:
+    return type(x).__module__.startswith("torch") and x.is_cuda
+
+
+def _kind(*bufs) -> str:
+    kinds = {("dev" if _is_dev(b) else "host") for b in bufs if b is not None}
+    if len(kinds) != 1:
+        raise TypeError("pass either all numpy arrays or all GPU torch tensors")
+    return kinds.pop()
+
+
+def _hp(a: np.ndarray) -> int:
+    if not isinstance(a, np.ndarray) or not a.flags["C_CONTIGUOUS"]:
+        raise TypeError("host buffers must be C-contiguous numpy arrays")
+    return a.ctypes.data
+
+
+def _dp(t) -> int:
+    if not t.is_contiguous():
+        raise TypeError("device buffers must be contiguous")
+    return t.data_ptr()
+
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _len(x) -> int:
+    return x.size if isinstance(x, np.ndarray) else x.numel()
+
+
+# --------------------------------------------------------------- wrappers
+def packed_a_len(m: int, k: int) -> int:
+    """Bytes of the tile-packed copy of an m x k activation (lib.rs:153-157)."""
+    return (m + 15) // 16 * 16 * k
+
+
+def pack_a(m: int, k: int, a, ap) -> None:
+    """Tile-pack int8 A (lib.rs:159-165)."""
+    assert k % 64 == 0
+    assert _len(a) >= m * k
+    assert _len(ap) >= packed_a_len(m, k)
+    backend()
+    if _kind(a, ap) == "host":
+        lib().fgm_pack_a_hip(m, k, _hp(a), _hp(ap))
+    else:
+        check(lib().fgm_hip_pack_a_dev(m, k, _dp(a), _dp(ap), _stream()))
+
+
+def gemm_q4g(m, n, k, a, a_scale, bq, b_scale, group, c, ldc, n0, n1) -> None:
+    """C[m, n] = (A int8 * a_scale) . (int4-grouped B * b_scale), columns
+    [n0*16, n1*16); `a` tile-packed (lib.rs:167-192).  b_scale: f16 bits."""
+    assert k % 64 == 0 and n % 16 == 0
+    assert (n1 - n0) % 4 == 0, "n-block range must be a multiple of 4"
+    backend()
+    if _kind(a, a_scale, bq, b_scale, c) == "host":
+        lib().fgm_gemm_q4g_hip(m, n, k, _hp(a), _hp(a_scale), _hp(bq), _hp(b_scale), group,
+                               _hp(c), ldc, n0, n1)
+    else:
+        check(lib().fgm_hip_gemm_q4g_dev(m, n, k, _dp(a), _dp(a_scale), _dp(bq), _dp(b_scale),
+                                         group, _dp(c), ldc, n0, n1, _stream()))
+
+
+def gemm_q8c(m, n, k, a, a_scale, b, b_scale, c, ldc, n0, n1) -> None:
+    """C[m, n] = (A int8 * a_scale) . (int8 per-channel B * b_scale)
+    (lib.rs:194-217)."""
+    assert k % 64 == 0 and n % 16 == 0
+    assert (n1 - n0) % 4 == 0, "n-block range must be a multiple of 4"
+    backend()
+    if _kind(a, a_scale, b, b_scale, c) == "host":
+        lib().fgm_gemm_q8c_hip(m, n, k, _hp(a), _hp(a_scale), _hp(b), _hp(b_scale), _hp(c),
+                               ldc, n0, n1)
+    else:
+        check(lib().fgm_hip_gemm_q8c_dev(m, n, k, _dp(a), _dp(a_scale), _dp(b), _dp(b_scale),
+                                         _dp(c), ldc, n0, n1, _stream()))
+
+
+def fwht(x, hsz: int) -> None:
+    """In-place normalised fast Walsh-Hadamard transform on blocks of hsz
+    (lib.rs:246-252)."""
+    n = _len(x)
+    assert hsz > 0 and n % hsz == 0 and (hsz & (hsz - 1)) == 0
+    backend()
+    if _kind(x) == "host":
+        lib().fgm_fwht_hip(_hp(x), n, hsz)
+    else:
+        check(lib().fgm_hip_fwht_dev(_dp(x), n, hsz, _stream()))
+
+
+def quant_act(x, rows: int, k: int, q, scale) -> None:
+    """Per-row symmetric int8 quantisation (lib.rs:254-257)."""
+    backend()
+    if _kind(x, q, scale) == "host":
+        lib().fgm_quant_act_hip(_hp(x), rows, k, _hp(q), _hp(scale))
+    else:
+        check(lib().fgm_hip_quant_act_dev(_dp(x), rows, k, _dp(q), _dp(scale), _stream()))
+
+
+def prep_rows(src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1) -> None:
+    """Rotate + quantise + tile-pack rows [r0, r1) of a GEMM activation
+    (lib.rs:510-529).  On the device path rot / qa may be None (not written)."""
+    assert r0 % 16 == 0, "prep row start must be tile-aligned"
+    backend()
+    if _kind(src, rot, qa, qs, pa) == "host":
+        lib().fgm_prep_rows_hip(_hp(src), lda, _hp(rot), _hp(qa), _hp(qs), _hp(pa), m, k, hsz,
+                                r0, r1)
+    else:
+        check(lib().fgm_hip_prep_rows_dev(_dp(src), lda, _dp(rot) if rot is not None else None,
+                                          _dp(qa) if qa is not None else None, _dp(qs), _dp(pa),
+                                          m, k, hsz, r0, r1, _stream()))
+
+
+# ------------------------------------------------- device-only extensions
+def acc_q8c(m, n, k, a, b, acc, ldacc, n0, n1) -> None:
+    """Raw int32 accumulators of the q8c GEMM (device tensors)."""
+    check(lib().fgm_hip_acc_q8c_dev(m, n, k, _dp(a), _dp(b), _dp(acc), ldacc, n0, n1, _stream()))
+
+
+def acc_q4g(m, n, k, a, bq, group, acc, ldacc, n0, n1) -> None:
+    """Raw per-group int32 accumulators of the q4g GEMM (device tensors),
+    acc[(g*m + row)*ldacc + col]."""
+    check(lib().fgm_hip_acc_q4g_dev(m, n, k, _dp(a), _dp(bq), group, _dp(acc), ldacc, n0, n1,
+                                    _stream()))
+
+
+def gemm_path(bits: int, m: int, k: int, group: int = 64) -> str:
+    """'skinny' or 'dense': which kernel family serves this shape."""
+    return ("skinny", "dense")[lib().fgm_hip_gemm_path(bits, m, k, group)]

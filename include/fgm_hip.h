@@ -1,0 +1,136 @@
+/*
+ * fgm_hip.h -- C ABI of the MI355X (gfx950) implementation of fastgemma's
+ * fgm-kernels quantized-matmul path.  Library: fastgemma_amd/libfgm_hip.so.
+ *
+ * Two layers:
+ *
+ *  1. Drop-in entry points.  Same parameter lists, argument meaning and
+ *     layouts as the reference's C symbols that the Rust crate binds in
+ *     crates/fgm-kernels/src/lib.rs:13-80; the suffix follows the reference's
+ *     `_vnni` convention (vnni_gemm.c:224,291).  All pointers are HOST
+ *     pointers.  Weight (B) and weight-scale buffers are treated as immutable
+ *     for the process lifetime -- they are the mmapped .fgm blobs
+ *     (model.rs:120-141, forward.rs:264-291) -- and are uploaded to the GPU on
+ *     first use and cached by host address.  A, scales and C move per call.
+ *     Like the reference (void returns, panic = "abort"), a failed
+ *     precondition or HIP call prints a message and aborts.
+ *
+ *  2. Device-resident API (fgm_hip_*).  Device pointers, an explicit HIP
+ *     stream (passed as void*; NULL = the null stream), int status (0 = ok,
+ *     otherwise an FGM_HIP_E* code with fgm_hip_last_error() describing it).
+ *     Launches are asynchronous on the given stream.  This is the layer the
+ *     benchmarks and a GPU-resident forward pass use.
+ *
+ * Layouts (unchanged from the .fgm file and the reference kernels):
+ *   packed A  [ceil(M/16)][K/64][16][64] int8, rows >= M zero (ops.c:279-290)
+ *   int8 B    [N/16][K/64] tiles of 1024 B, (K=64,N=16) as [k/4][n][k%4]
+ *             (quant.py:96-107); b_scale f32 [N]
+ *   int4 B    the int8 stream nibble-packed per 64-B block,
+ *             packed[i] = q[i] & 15 | q[i+32] << 4 (quant.py:76-82), two's
+ *             complement nibbles; b_scale f16 bits [K/group][N] (quant.py:165)
+ *   C         f32 [M][ldc]; only rows < M and columns [16*n0, 16*n1) written.
+ *
+ * Preconditions (the reference asserts them in debug Rust only,
+ * lib.rs:161-163,176-177,201-202,521; they are always checked here):
+ *   K % 64 == 0, N % 16 == 0, 0 <= n0 <= n1 <= N/16, (n1 - n0) % 4 == 0,
+ *   ldc >= N... (ldc >= 16*n1), q4g: group % 64 == 0 and K % group == 0,
+ *   prep_rows: r0 % 16 == 0, k % 64 == 0; fwht: hsz a power of two, n % hsz == 0.
+ */
+#ifndef FGM_HIP_H
+#define FGM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status codes */
+#define FGM_HIP_OK 0
+#define FGM_HIP_EINVAL 1   /* a precondition on shapes / pointers failed   */
+#define FGM_HIP_EHIP 2     /* a HIP runtime call failed                     */
+#define FGM_HIP_ENODEV 3   /* no usable gfx950 device                       */
+
+/* ================================================================ drop-in */
+
+/* replaces fgm_pack_a (lib.rs:19; ops.c:279-290) */
+void fgm_pack_a_hip(int m, int k, const int8_t *a, int8_t *ap);
+
+/* replaces fgm_prep_rows (lib.rs:20-23; ops.c:293-314) */
+void fgm_prep_rows_hip(const float *src, int lda, float *rot, int8_t *qa, float *qs,
+                       int8_t *pa, int m, int k, int hsz, int r0, int r1);
+
+/* replaces fgm_gemm_q4g / fgm_gemm_q4g_vnni (lib.rs:24-28,36-40;
+ * amx_gemm.c:333-372, vnni_gemm.c:291-322).  b_scale: f16 bits. */
+void fgm_gemm_q4g_hip(int m, int n, int k, const int8_t *a, const float *a_scale,
+                      const uint8_t *bq, const uint16_t *b_scale, int group, float *c,
+                      int ldc, int n0, int n1);
+
+/* replaces fgm_gemm_q8c / fgm_gemm_q8c_vnni (lib.rs:29-33,41-45;
+ * amx_gemm.c:444-475, vnni_gemm.c:224-245) */
+void fgm_gemm_q8c_hip(int m, int n, int k, const int8_t *a, const float *a_scale,
+                      const int8_t *b, const float *b_scale, float *c, int ldc, int n0,
+                      int n1);
+
+/* replaces fgm_fwht (lib.rs:52; ops.c:153-175) */
+void fgm_fwht_hip(float *x, int n, int hsz);
+
+/* replaces fgm_quant_act (lib.rs:53; ops.c:181-204) */
+void fgm_quant_act_hip(const float *x, int rows, int k, int8_t *q, float *scale);
+
+/* replaces fgm_cpu_has_amx / fgm_cpu_has_avx512_vnni as the backend probe
+ * (lib.rs:34-35,112-137): 1 when a gfx950 device is usable, else 0. */
+int fgm_hip_available(void);
+
+/* Drop the cached device copies of host weight buffers (for callers that
+ * unmap or rewrite a weight file). */
+void fgm_hip_weight_cache_clear(void);
+
+/* ======================================================= device-resident */
+
+/* Select and check the device (gfx950).  Optional: every entry point
+ * initialises the current device on first use. */
+int fgm_hip_init(int device);
+
+/* Message for the last non-zero status returned on this thread. */
+const char *fgm_hip_last_error(void);
+
+int fgm_hip_gemm_q8c_dev(int m, int n, int k, const int8_t *a, const float *a_scale,
+                         const int8_t *b, const float *b_scale, float *c, int ldc, int n0,
+                         int n1, void *stream);
+
+int fgm_hip_gemm_q4g_dev(int m, int n, int k, const int8_t *a, const float *a_scale,
+                         const uint8_t *bq, const uint16_t *b_scale, int group, float *c,
+                         int ldc, int n0, int n1, void *stream);
+
+/* Raw int32 accumulators (no reference counterpart: the reference never
+ * exposes them; this is the evidence for "int32 bit-exact").
+ *   q8c: acc[m * ldacc + n]              = sum_k A[m][k] * B[k][n]
+ *   q4g: acc[(g * M + m) * ldacc + n]    = sum_{k in group g} A[m][k] * B[k][n]
+ * for m < M, n in [16*n0, 16*n1). */
+int fgm_hip_acc_q8c_dev(int m, int n, int k, const int8_t *a, const int8_t *b, int32_t *acc,
+                        int ldacc, int n0, int n1, void *stream);
+int fgm_hip_acc_q4g_dev(int m, int n, int k, const int8_t *a, const uint8_t *bq, int group,
+                        int32_t *acc, int ldacc, int n0, int n1, void *stream);
+
+/* fgm_prep_rows on device buffers.  rot and qa may be NULL (not written);
+ * the reference always writes them.  pa rows of r1's tile block that lie in
+ * [r1, m) are copied from qa, which must then be non-NULL (ops.c:308-311). */
+int fgm_hip_prep_rows_dev(const float *src, int lda, float *rot, int8_t *qa, float *qs,
+                          int8_t *pa, int m, int k, int hsz, int r0, int r1, void *stream);
+
+int fgm_hip_quant_act_dev(const float *x, int rows, int k, int8_t *q, float *scale,
+                          void *stream);
+int fgm_hip_pack_a_dev(int m, int k, const int8_t *a, int8_t *ap, void *stream);
+int fgm_hip_fwht_dev(float *x, int n, int hsz, void *stream);
+
+/* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
+ * kernel, 1 = dense MFMA kernel. */
+int fgm_hip_gemm_path(int bits, int m, int k, int group);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FGM_HIP_H */

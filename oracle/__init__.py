@@ -15,8 +15,8 @@ Two CPU implementations are reachable from here:
   files travel with the tree).  ``ref()`` / ``ref_amx()`` return ``None`` when a
   library is missing or the host CPU lacks the ISA it needs.
 
-Pinning status of each oracle function is listed in ``__all__``'s functions'
-docstrings and checked by ``tests/test_oracle.py``.
+How each oracle function is pinned (reference outputs, known answers, closed
+forms, brute force) is documented and checked in ``tests/test_oracle.py``.
 """
 from __future__ import annotations
 
@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
         L.orc_gemm_q8c.argtypes = [_i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _i]
         L.orc_acc_q4g.argtypes = [_i, _i, _p, _p, _i, _p, _i, _i, _i]
         L.orc_gemm_q4g.argtypes = [_i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _i, _i]
+        L.orc_epilogue_q8c.argtypes = [_i, _p, _i, _p, _p, _p, _i, _i, _i]
+        L.orc_epilogue_q4g.argtypes = [_i, _i, _i, _p, _i, _p, _p, _p, _i, _i, _i]
         L.orc_gen_i8.argtypes = [_u64, _sz, _i, _i, _p]
         L.orc_gen_u8.argtypes = [_u64, _sz, _p]
         L.orc_gen_uniform.argtypes = [_u64, _sz, _f, _f, _p]
@@ -273,6 +275,19 @@ def acc_q4g(m, k, ap, bq, group, n0, n1, ldacc):
     acc = np.zeros((k // group, m, ldacc), np.int32)
     lib().orc_acc_q4g(m, k, _ptr(ap), _ptr(bq), group, _ptr(acc), ldacc, n0, n1)
     return acc
+
+
+def epilogue_q8c(m, acc, ldacc, a_scale, b_scale, c, ldc, n0, n1) -> None:
+    """q8c epilogue (vnni_gemm.c:206-219) on given int32 accumulators."""
+    lib().orc_epilogue_q8c(m, _ptr(acc), ldacc, _ptr(a_scale), _ptr(b_scale), _ptr(c), ldc,
+                           n0, n1)
+
+
+def epilogue_q4g(m, n, ng, acc, ldacc, a_scale, b_scale, c, ldc, n0, n1) -> None:
+    """q4g group chain (vnni_gemm.c:258-285, 316-321) on given per-group
+    accumulators acc[(g*m + row)*ldacc + col]."""
+    lib().orc_epilogue_q4g(m, n, ng, _ptr(acc), ldacc, _ptr(a_scale), _ptr(b_scale), _ptr(c),
+                           ldc, n0, n1)
 
 
 def gemm_q8c(m, n, k, ap, a_scale, b, b_scale, c, ldc, n0, n1) -> None:

@@ -268,20 +268,28 @@ void orc_acc_q8c(int M, int K, const int8_t *Ap, const int8_t *B, int32_t *acc, 
     }
 }
 
+/* The q8c epilogue on given accumulators, vnni_gemm.c:206-219:
+ * C[m][n] = (float)acc * (b_scale[n] * a_scale[m]) -- the scale product is
+ * rounded first, the int32 -> float conversion rounds to nearest even. */
+void orc_epilogue_q8c(int M, const int32_t *acc, int ldacc, const float *a_scale,
+                      const float *b_scale, float *C, int ldc, int n0, int n1) {
+  for (int m = 0; m < M; m++)
+    for (int n = n0 * 16; n < n1 * 16; n++) {
+      float f = (float)acc[(size_t)m * ldacc + n];
+      float sc = b_scale[n] * a_scale[m];
+      C[(size_t)m * ldc + n] = f * sc;
+    }
+}
+
 /* fgm_gemm_q8c_vnni, vnni_gemm.c:224-245 (+ q8c_block :190-222).
  * Writes C[m][n] for m < M, n in [16*n0, 16*n1); nothing else is touched. */
 void orc_gemm_q8c(int M, int N, int K, const int8_t *Ap, const float *a_scale,
                   const int8_t *B, const float *b_scale, float *C, int ldc, int n0, int n1) {
-  (void)N;
-  for (int m = 0; m < M; m++)
-    for (int n = n0 * 16; n < n1 * 16; n++) {
-      uint32_t s = 0;
-      for (int k = 0; k < K; k++)
-        s += (uint32_t)((int32_t)apk(Ap, K, m, k) * (int32_t)B[b8_off(K, k, n)]);
-      float f = (float)(int32_t)s;
-      float sc = b_scale[n] * a_scale[m];
-      C[(size_t)m * ldc + n] = f * sc;
-    }
+  if (M <= 0 || n1 <= n0) return;
+  int32_t *acc = (int32_t *)malloc((size_t)M * N * sizeof(int32_t));
+  orc_acc_q8c(M, K, Ap, B, acc, N, n0, n1);
+  orc_epilogue_q8c(M, acc, N, a_scale, b_scale, C, ldc, n0, n1);
+  free(acc);
 }
 
 /* Raw per-group int32 accumulators of the q4g GEMM:
@@ -299,26 +307,36 @@ void orc_acc_q4g(int M, int K, const int8_t *Ap, const uint8_t *Bq, int group, i
       }
 }
 
-/* fgm_gemm_q4g_vnni, vnni_gemm.c:291-322 (+ q4g_block :252-289).
- * b_scale is f16 [K/group][N]. */
-void orc_gemm_q4g(int M, int N, int K, const int8_t *Ap, const float *a_scale,
-                  const uint8_t *Bq, const uint16_t *b_scale, int group, float *C, int ldc,
-                  int n0, int n1) {
-  const int NG = K / group;
+/* The q4g epilogue on given per-group accumulators (acc laid out as
+ * orc_acc_q4g writes it), vnni_gemm.c:258-285 and 316-321: C = 0, then per
+ * group g in ascending order C = fmaf((float)acc_g, f16(b_scale[g][n]), C),
+ * finally C *= a_scale[m]. */
+void orc_epilogue_q4g(int M, int N, int NG, const int32_t *acc, int ldacc, const float *a_scale,
+                      const uint16_t *b_scale, float *C, int ldc, int n0, int n1) {
   for (int m = 0; m < M; m++)
     for (int n = n0 * 16; n < n1 * 16; n++) {
       float c = 0.0f;
-      for (int g = 0; g < NG; g++) {
-        uint32_t s = 0;
-        for (int k = g * group; k < (g + 1) * group; k++)
-          s += (uint32_t)((int32_t)apk(Ap, K, m, k) * b4_val(Bq, K, k, n));
-        c = fmaf((float)(int32_t)s, orc_f16_to_f32(b_scale[(size_t)g * N + n]), c);
-      }
+      for (int g = 0; g < NG; g++)
+        c = fmaf((float)acc[((size_t)g * M + m) * ldacc + n],
+                 orc_f16_to_f32(b_scale[(size_t)g * N + n]), c);
       C[(size_t)m * ldc + n] = c;
     }
   for (int m = 0; m < M; m++)
     for (int n = n0 * 16; n < n1 * 16; n++)
       C[(size_t)m * ldc + n] = C[(size_t)m * ldc + n] * a_scale[m];
+}
+
+/* fgm_gemm_q4g_vnni, vnni_gemm.c:291-322 (+ q4g_block :252-289).
+ * b_scale is f16 [K/group][N]. */
+void orc_gemm_q4g(int M, int N, int K, const int8_t *Ap, const float *a_scale,
+                  const uint8_t *Bq, const uint16_t *b_scale, int group, float *C, int ldc,
+                  int n0, int n1) {
+  if (M <= 0 || n1 <= n0) return;
+  const int NG = K / group;
+  int32_t *acc = (int32_t *)malloc((size_t)(NG ? NG : 1) * M * N * sizeof(int32_t));
+  orc_acc_q4g(M, K, Ap, Bq, group, acc, N, n0, n1);
+  orc_epilogue_q4g(M, N, NG, acc, N, a_scale, b_scale, C, ldc, n0, n1);
+  free(acc);
 }
 
 /* ------------------------------------------------------------ generators */

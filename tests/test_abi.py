@@ -1,0 +1,106 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol that
+include/fgm_hip.h declares, refuses bad shapes before touching a device, and
+reports the absence of a GPU instead of falling back to anything."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import fastgemma_amd as F
+from fastgemma_amd import kernels as K
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fgm_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fgm_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = F.lib()
+    names = declared_symbols()
+    assert len(names) >= 18
+    for name in names:
+        assert hasattr(L, name), name
+
+
+def test_dropin_symbols_mirror_reference_names():
+    """Every GEMM-path symbol the reference's Rust crate binds (lib.rs:19-53)
+    has a _hip twin."""
+    ref = ["fgm_pack_a", "fgm_prep_rows", "fgm_gemm_q4g", "fgm_gemm_q8c", "fgm_fwht",
+           "fgm_quant_act"]
+    names = declared_symbols()
+    for r in ref:
+        assert r + "_hip" in names
+
+
+BAD_Q8C = [
+    dict(m=8, n=256, k=100, ldc=256, n0=0, n1=16),   # k % 64
+    dict(m=8, n=250, k=128, ldc=256, n0=0, n1=15),   # n % 16
+    dict(m=8, n=256, k=128, ldc=256, n0=0, n1=6),    # (n1 - n0) % 4
+    dict(m=8, n=256, k=128, ldc=256, n0=4, n1=20),   # n1 > n / 16
+    dict(m=8, n=256, k=128, ldc=100, n0=0, n1=16),   # ldc < 16 n1
+    dict(m=-1, n=256, k=128, ldc=256, n0=0, n1=16),  # negative
+]
+
+
+@pytest.mark.parametrize("args", BAD_Q8C)
+def test_bad_shapes_are_refused_with_einval(args):
+    L = F.lib()
+    rc = L.fgm_hip_gemm_q8c_dev(args["m"], args["n"], args["k"], None, None, None, None, None,
+                                args["ldc"], args["n0"], args["n1"], None)
+    assert rc == 1, L.fgm_hip_last_error()
+    assert L.fgm_hip_last_error()
+
+
+@pytest.mark.parametrize("group", [0, 32, 96, 192])
+def test_bad_group_is_refused(group):
+    L = F.lib()
+    rc = L.fgm_hip_gemm_q4g_dev(8, 256, 1024, None, None, None, None, group, None, 256, 0, 16,
+                                None)
+    assert rc == 1 and b"group" in L.fgm_hip_last_error()
+
+
+def test_other_preconditions():
+    L = F.lib()
+    assert L.fgm_hip_prep_rows_dev(None, 64, None, None, None, None, 32, 64, 0, 8, 16, None) == 1
+    assert L.fgm_hip_prep_rows_dev(None, 64, None, None, None, None, 32, 100, 0, 0, 16, None) == 1
+    assert L.fgm_hip_prep_rows_dev(None, 128, None, None, None, None, 32, 128, 48, 0, 16, None) == 1
+    assert L.fgm_hip_fwht_dev(None, 96, 12, None) == 1
+    assert L.fgm_hip_fwht_dev(None, 96, 64, None) == 1
+    assert L.fgm_hip_pack_a_dev(4, 100, None, None, None) == 1
+
+
+def test_no_gpu_means_no_backend():
+    """On a host without a gfx950 device the library says so; nothing runs on
+    the CPU in its place."""
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    L = F.lib()
+    assert L.fgm_hip_available() == 0
+    rc = L.fgm_hip_gemm_q8c_dev(8, 256, 128, None, None, None, None, None, 256, 0, 16, None)
+    assert rc == 3  # FGM_HIP_ENODEV, after the shape checks passed
+    with pytest.raises(F.HipUnavailable):
+        K.backend()
+
+
+def test_skinny_dense_dispatch_thresholds():
+    assert K.gemm_path(8, 1, 2048) == "skinny"
+    assert K.gemm_path(4, 8, 8192, 64) == "skinny"
+    assert K.gemm_path(8, 64, 2048) == "skinny"
+    assert K.gemm_path(8, 65, 2048) == "dense"
+    assert K.gemm_path(4, 256, 2048, 64) == "dense"
+    # the int4 skinny kernel keeps every group's sums in LDS; past 160 KB it goes dense
+    assert K.gemm_path(4, 64, 65536, 64) == "dense"
