@@ -184,7 +184,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int MT, int NT, i
     const int nb = nb0 + wn * 4 + ns;
     if (nb >= nbend) continue;
     const int n = nb * 16 + j;
-    const float bsn = (BITS == 8) ? ((const float*)a.b_scale)[n] : 0.0f;
+    // raw-accumulator mode passes no scales
+    const float bsn = (BITS == 8 && !a.acc_out) ? ((const float*)a.b_scale)[n] : 0.0f;
 #pragma unroll
     for (int ms = 0; ms < 4; ms++)
 #pragma unroll
