@@ -1,0 +1,484 @@
+"""Benchmark of the fgm-kernels quantized-matmul path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+
+Headline workload: batched decode skinny GEMM,
+M = 8 activation rows ~ N(0,1) fp32, int4 weights group 64 with f16 scales,
+two shapes -- up N=8192 K=2048 and down N=2048 K=8192.  One step = the hot
+path over one batch: for each shape, quantise + tile-pack the fp32 rows
+(prep kernel) and run the int4 GEMM with its fp32 epilogue.  Weights rotate
+over 48 distinct copies (~870 MB), so no step finds its weights in the
+256 MB MALL; inputs are resident in HBM before the timed region.  Steps are
+launched as HIP graphs (torch.cuda.CUDAGraph is only the capture/replay
+plumbing) so host launch overhead stays off the GPU timeline.
+
+`value` = algorithmic bytes per step / step time, in GB/s, where the bytes are
+weights + f16 scales + packed A + a_scale + f32 C of both GEMMs plus the
+prep's fp32 read and packed-A write.
+
+`roofline` is for the dominant kernel (the int4 skinny GEMM, up shape): the
+average duration of one launch, measured with HIP events around a graph of
+48 back-to-back launches on the launch stream; `traffic` comes from the
+committed rocprofv3 PMC summary when present.
+
+`cpu_baseline` runs the reference's own VNNI kernels (oracle/_ref, compiled
+from the reference sources) on this host's cores with the reference's thread
+split, on the same shapes, for about 10 s; falls back to the oracle port.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+I8_PEAK = 5.0e15         # dense int8 MFMA ops/s (MI355X, no sparsity)
+NCOPY = 48
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------- byte counts
+def gemm_bytes(bits, M, N, K, group=64):
+    """Algorithmic bytes of one GEMM launch: weights + scales + packed A +
+    a_scale + C (fp32).  Packed A counts the rows the layout stores."""
+    w = N * K if bits == 8 else N * K // 2
+    s = N * 4 if bits == 8 else (K // group) * N * 2
+    mp = (M + 15) // 16 * 16
+    return w + s + mp * K + 4 * M + 4 * M * N
+
+
+def prep_bytes(M, K):
+    mp = (M + 15) // 16 * 16
+    return 4 * M * K + mp * K + 4 * M
+
+
+# ---------------------------------------------------------------- plumbing
+class Gpu:
+    def __init__(self):
+        import torch
+        import fastgemma_amd as F
+        from fastgemma_amd import kernels
+        self.t = torch
+        self.F = F
+        self.L = F.lib()
+        kernels.backend()
+        self.dev = torch.device("cuda:0")
+
+    def stream(self):
+        return self.t.cuda.current_stream().cuda_stream
+
+    def prep(self, x, qs, pa, M, K):
+        rc = self.L.fgm_hip_prep_rows_dev(x.data_ptr(), K, None, None, qs.data_ptr(),
+                                          pa.data_ptr(), M, K, 0, 0, M, self.stream())
+        self.F.check(rc)
+
+    def prep_many(self, items):
+        """items: (x, qs, pa, M, K) -- one launch for all."""
+        arr = (self.F.PrepDesc * len(items))()
+        for i, (x, qs, pa, M, K) in enumerate(items):
+            arr[i] = self.F.PrepDesc(x.data_ptr(), K, None, None, qs.data_ptr(), pa.data_ptr(),
+                                     M, K, 0, 0, M)
+        self.F.check(self.L.fgm_hip_prep_batch_dev(arr, len(items), self.stream()))
+
+    def gemm_many(self, items):
+        """items: (bits, M, N, K, pa, qs, w, s, c) -- as few launches as possible."""
+        arr = (self.F.GemmDesc * len(items))()
+        for i, (bits, M, N, K, pa, qs, w, s, c) in enumerate(items):
+            arr[i] = self.F.GemmDesc(bits, M, N, K, 64, pa.data_ptr(), qs.data_ptr(), w.data_ptr(),
+                                     s.data_ptr(), c.data_ptr(), N, 0, N // 16)
+        self.F.check(self.L.fgm_hip_gemm_batch_dev(arr, len(items), self.stream()))
+
+    def q4g(self, M, N, K, pa, qs, w, s, c, group=64):
+        rc = self.L.fgm_hip_gemm_q4g_dev(M, N, K, pa.data_ptr(), qs.data_ptr(), w.data_ptr(),
+                                         s.data_ptr(), group, c.data_ptr(), N, 0, N // 16,
+                                         self.stream())
+        self.F.check(rc)
+
+    def q8c(self, M, N, K, pa, qs, w, s, c):
+        rc = self.L.fgm_hip_gemm_q8c_dev(M, N, K, pa.data_ptr(), qs.data_ptr(), w.data_ptr(),
+                                         s.data_ptr(), c.data_ptr(), N, 0, N // 16, self.stream())
+        self.F.check(rc)
+
+    # synthetic operands, generated on the device
+    def w4(self, N, K, group=64):
+        t = self.t
+        w = t.randint(0, 256, (N * K // 2,), dtype=t.uint8, device=self.dev)
+        s = (t.rand((K // group) * N, device=self.dev) * 0.045 + 0.005).half().view(t.int16)
+        return w, s
+
+    def w8(self, N, K):
+        t = self.t
+        w = t.randint(-127, 128, (N * K,), dtype=t.int8, device=self.dev)
+        s = t.rand(N, device=self.dev) * 0.009 + 0.001
+        return w, s
+
+    def act(self, M, K):
+        t = self.t
+        x = t.randn(M, K, device=self.dev)
+        qs = t.empty(M, device=self.dev)
+        pa = t.empty((M + 15) // 16 * 16 * K, dtype=t.int8, device=self.dev)
+        return x, qs, pa
+
+    def graphs(self, fn, nsteps, chunk):
+        """Capture fn(i) for i in [0, nsteps) as graphs of `chunk` steps."""
+        t = self.t
+        s = t.cuda.Stream()
+        s.wait_stream(t.cuda.current_stream())
+        with t.cuda.stream(s):
+            for i in range(min(3, nsteps)):
+                fn(i)
+        t.cuda.current_stream().wait_stream(s)
+        t.cuda.synchronize()
+        out = []
+        for b in range(0, nsteps, chunk):
+            g = t.cuda.CUDAGraph()
+            with t.cuda.graph(g):
+                for i in range(b, min(nsteps, b + chunk)):
+                    fn(i)
+            out.append(g)
+        t.cuda.synchronize()
+        return out
+
+    def time_graphs(self, gs, reps=1):
+        """Seconds for `reps` passes over the graph list, HIP events on the
+        replay stream, synchronize on both sides."""
+        t = self.t
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for g in gs:
+                g.replay()
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3
+
+
+# ------------------------------------------------------------- workloads
+def cfg2_setup(gpu):
+    ups = [gpu.w4(8192, 2048) for _ in range(NCOPY)]
+    downs = [gpu.w4(2048, 8192) for _ in range(NCOPY)]
+    xu, qsu, pau = gpu.act(8, 2048)
+    xd, qsd, pad_ = gpu.act(8, 8192)
+    cu = gpu.t.empty(8, 8192, device=gpu.dev)
+    cd = gpu.t.empty(8, 2048, device=gpu.dev)
+
+    def gemms(c):
+        return [(4, 8, 8192, 2048, pau, qsu, ups[c][0], ups[c][1], cu),
+                (4, 8, 2048, 8192, pad_, qsd, downs[c][0], downs[c][1], cd)]
+
+    def step(i):
+        # one prep launch for both activations, one GEMM launch for both shapes
+        gpu.prep_many([(xu, qsu, pau, 8, 2048), (xd, qsd, pad_, 8, 8192)])
+        gpu.gemm_many(gemms(i % NCOPY))
+
+    def gemv_pair(i):
+        gpu.gemm_many(gemms(i % NCOPY))
+
+    def gemv_up(i):
+        c = i % NCOPY
+        gpu.q4g(8, 8192, 2048, pau, qsu, ups[c][0], ups[c][1], cu)
+
+    def gemv_down(i):
+        c = i % NCOPY
+        gpu.q4g(8, 2048, 8192, pad_, qsd, downs[c][0], downs[c][1], cd)
+
+    step_bytes = (gemm_bytes(4, 8, 8192, 2048) + gemm_bytes(4, 8, 2048, 8192)
+                  + prep_bytes(8, 2048) + prep_bytes(8, 8192))
+    host = dict(up=(ups[0][0].cpu().numpy(), ups[0][1].cpu().numpy()),
+                down=(downs[0][0].cpu().numpy(), downs[0][1].cpu().numpy()))
+    return step, gemv_pair, gemv_up, gemv_down, step_bytes, host
+
+
+def kernel_avg(gpu, fn, n=NCOPY, reps=5):
+    """Average seconds per launch of fn over a graph of n back-to-back launches."""
+    gs = gpu.graphs(fn, n, n)
+    gpu.time_graphs(gs, 2)
+    return gpu.time_graphs(gs, reps) / (reps * n)
+
+
+def extra_cfg1(gpu):
+    ws = [gpu.w8(8192, 2048) for _ in range(24)]   # 24 x 16.8 MB = 403 MB > MALL
+    x, qs, pa = gpu.act(1, 2048)
+    c = gpu.t.empty(1, 8192, device=gpu.dev)
+    gpu.prep(x, qs, pa, 1, 2048)
+    dt = kernel_avg(gpu, lambda i: gpu.q8c(1, 8192, 2048, pa, qs, ws[i % 24][0], ws[i % 24][1], c), 24)
+    b = gemm_bytes(8, 1, 8192, 2048)
+    return {"workload": "int8 GEMV M=1 N=8192 K=2048", "us_per_launch": dt * 1e6,
+            "GB_s": b / dt / 1e9, "frac_hbm": b / dt / HBM_PEAK, "bytes_per_launch": b}
+
+
+LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048),
+         ("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
+
+
+def extra_cfg3(gpu):
+    ncp = 5                                         # 5 x 58 MB of int8 layers > MALL
+    res, tot_ops, tot_t = {}, 0.0, 0.0
+    xs = {K: gpu.act(256, K) for K in (2048, 8192)}
+    for K, (x, qs, pa) in xs.items():
+        gpu.prep(x, qs, pa, 256, K)
+    for name, N, K in LAYER:
+        ws = [gpu.w8(N, K) for _ in range(ncp)]
+        x, qs, pa = xs[K]
+        c = gpu.t.empty(256, N, device=gpu.dev)
+        dt = kernel_avg(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[i % ncp][0], ws[i % ncp][1], c), 20)
+        ops = 2.0 * 256 * N * K
+        res[name] = {"us": dt * 1e6, "TOPS": ops / dt / 1e12, "frac_mfma": ops / dt / I8_PEAK}
+        tot_ops += ops
+        tot_t += dt
+        del ws
+    return {"workload": "int8 prefill M=256, 7 projection shapes of one layer",
+            "per_shape": res, "layer_us": tot_t * 1e6, "TOPS": tot_ops / tot_t / 1e12,
+            "frac_mfma": tot_ops / tot_t / I8_PEAK,
+            "tokens_per_s_30_layers": 256 / (30 * tot_t)}
+
+
+def extra_cfg4(gpu):
+    """30 synthetic layers (q,k,v,o,gate,up int4 g64; down int8) + int8 LM
+    head [262144, 2048], M = 8, distinct buffers, one graph per step."""
+    layers = []
+    for _ in range(30):
+        L = {}
+        for name, N, K in LAYER:
+            L[name] = gpu.w8(N, K) if name == "down" else gpu.w4(N, K)
+        layers.append(L)
+    head = gpu.w8(262144, 2048)
+    a2 = gpu.act(8, 2048)
+    a8 = gpu.act(8, 8192)
+    outs = {name: gpu.t.empty(8, N, device=gpu.dev) for name, N, K in LAYER}
+    logits = gpu.t.empty(8, 262144, device=gpu.dev)
+
+    def w(L, name, bits, pa, qs):
+        N, K = next((N, K) for nm, N, K in LAYER if nm == name)
+        return (bits, 8, N, K, pa, qs, L[name][0], L[name][1], outs[name])
+
+    def step(_i):
+        # the reference forward's GEMM sequence per layer (forward.rs:484-641):
+        # q/k/v on one activation, o, gate/up on one activation, down
+        x, qs, pa = a2
+        xd, qsd, pad_ = a8
+        for L in layers:
+            gpu.prep(x, qs, pa, 8, 2048)                  # attention input
+            gpu.gemm_many([w(L, "q", 4, pa, qs), w(L, "k", 4, pa, qs), w(L, "v", 4, pa, qs)])
+            gpu.prep(x, qs, pa, 8, 2048)                  # attention output
+            gpu.gemm_many([w(L, "o", 4, pa, qs)])
+            gpu.prep(x, qs, pa, 8, 2048)                  # FFN input
+            gpu.gemm_many([w(L, "gate", 4, pa, qs), w(L, "up", 4, pa, qs)])
+            gpu.prep(xd, qsd, pad_, 8, 8192)             # FFN hidden
+            gpu.gemm_many([w(L, "down", 8, pad_, qsd)])
+        gpu.prep(x, qs, pa, 8, 2048)
+        gpu.q8c(8, 262144, 2048, pa, qs, head[0], head[1], logits)
+
+    gs = gpu.graphs(step, 1, 1)
+    gpu.time_graphs(gs, 3)
+    reps = 20
+    dt = gpu.time_graphs(gs, reps) / reps
+    wbytes = 0
+    for name, N, K in LAYER:
+        wbytes += (N * K + N * 4) if name == "down" else (N * K // 2 + (K // 64) * N * 2)
+    wbytes = wbytes * 30 + 262144 * 2048 + 262144 * 4
+    allb = 0
+    for name, N, K in LAYER:
+        allb += gemm_bytes(8 if name == "down" else 4, 8, N, K)
+    allb = allb * 30 + gemm_bytes(8, 8, 262144, 2048) + 30 * (3 * prep_bytes(8, 2048) + prep_bytes(8, 8192)) + prep_bytes(8, 2048)
+    return {"workload": "decode step M=8: 30 layers + int8 LM head, 242 launches (q/k/v and "
+                        "gate/up batched), one graph",
+            "us_per_step": dt * 1e6, "weight_bytes": wbytes, "GB_s_weights": wbytes / dt / 1e9,
+            "GB_s_all": allb / dt / 1e9, "frac_hbm": allb / dt / HBM_PEAK,
+            "tokens_per_s": 8 / dt}
+
+
+def extra_cfg5(gpu):
+    res = {}
+    x2, qs2, pa2 = gpu.act(2048, 2048)
+    x8, qs8, pa8 = gpu.act(2048, 8192)
+    gpu.prep(x2, qs2, pa2, 2048, 2048)
+    gpu.prep(x8, qs8, pa8, 2048, 8192)
+    for name, bits, N, K in (("gate", 4, 8192, 2048), ("up", 4, 8192, 2048), ("down", 8, 2048, 8192)):
+        ws = [gpu.w4(N, K) if bits == 4 else gpu.w8(N, K) for _ in range(2)]
+        c = gpu.t.empty(2048, N, device=gpu.dev)
+        if bits == 4:
+            fn = lambda i: gpu.q4g(2048, N, K, pa2, qs2, ws[i % 2][0], ws[i % 2][1], c)
+        else:
+            fn = lambda i: gpu.q8c(2048, N, K, pa8, qs8, ws[i % 2][0], ws[i % 2][1], c)
+        dt = kernel_avg(gpu, fn, 8, 3)
+        ops = 2.0 * 2048 * N * K
+        res[name] = {"bits": bits, "us": dt * 1e6, "TOPS": ops / dt / 1e12,
+                     "frac_mfma": ops / dt / I8_PEAK}
+    return {"workload": "long prefill M=2048 (gate/up int4 g64, down int8)", "per_shape": res}
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(host, budget_s=10.0):
+    import numpy as np
+    import oracle
+    L = oracle.lib()
+    R = oracle.ref()
+    nt = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    nt = max(1, min(nt, 64))
+    L.orc_pool_start(nt)
+    kind = "reference" if R is not None else "port"
+    if R is not None:
+        fq4 = C.cast(R.fgm_gemm_q4g_vnni, C.c_void_p).value
+        fprep = C.cast(R.fgm_prep_rows, C.c_void_p).value
+    else:
+        fq4 = C.cast(L.orc_gemm_q4g, C.c_void_p).value
+        fprep = C.cast(L.orc_prep_rows, C.c_void_p).value
+    P = oracle._ptr
+    shapes = (("up", 8192, 2048), ("down", 2048, 8192))
+    bufs = {}
+    for name, N, K in shapes:
+        w, s = host[name]
+        x = oracle.gen_normal(5, 8 * K).reshape(8, K)
+        bufs[name] = dict(w=np.ascontiguousarray(w), s=np.ascontiguousarray(s), x=x,
+                          rot=np.empty((8, K), np.float32), qa=np.empty((8, K), np.int8),
+                          qs=np.empty(8, np.float32), pa=np.empty(16 * K, np.int8),
+                          c=np.empty((8, N), np.float32), N=N, K=K)
+    t1 = np.empty(1, np.float64)
+
+    def one_step():
+        for name, N, K in shapes:
+            b = bufs[name]
+            L.orc_pool_prep(fprep, P(b["x"]), K, P(b["rot"]), P(b["qa"]), P(b["qs"]), P(b["pa"]),
+                            8, K, 0, 1, P(t1))
+            L.orc_pool_q4g(fq4, 8, N, K, P(b["pa"]), P(b["qs"]), P(b["w"]), P(b["s"]), 64,
+                           P(b["c"]), N, 1, P(t1))
+
+    one_step()  # warm-up pass over the weights
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 10:
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+    L.orc_pool_stop()
+    med = sorted(times)[len(times) // 2]
+    step_bytes = (gemm_bytes(4, 8, 8192, 2048) + gemm_bytes(4, 8, 2048, 8192)
+                  + prep_bytes(8, 2048) + prep_bytes(8, 8192))
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    amx = bool(R is not None and R.fgm_cpu_has_amx())
+    return {"value": step_bytes / med / 1e9, "unit": "GB/s", "cores": nt, "kind": kind,
+            "sample": f"{len(times)} steps of cfg2 (prep + q4g up + prep + q4g down, M=8) in "
+                      f"~{budget_s:.0f} s, median step {med * 1e3:.3f} ms; reference "
+                      f"fgm_prep_rows + fgm_gemm_q4g_vnni, pool.rs N-split over {nt} threads; "
+                      f"host '{cpu}', AMX present: {amx} (AMX path not timed)"}
+
+
+# ------------------------------------------------------------------ main
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed PMC
+    summary (profiles/decode_q4g_m8_up_traffic.txt), or None."""
+    p = os.path.join(ROOT, "profiles", "decode_q4g_m8_up_traffic.txt")
+    try:
+        for line in open(p):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=480)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the N-sharded design is described in DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    gpu = Gpu()
+    gpu.t.manual_seed(1234)
+    log("setting up cfg2 (48 weight copies)")
+    step, gemv_pair, gemv_up, gemv_down, step_bytes, host = cfg2_setup(gpu)
+
+    chunk = 16
+    warm = gpu.graphs(step, max(chunk, args.warmup), chunk)
+    gpu.time_graphs(warm)
+    # exactly `steps` steps: full chunks plus one remainder graph
+    gs = gpu.graphs(step, args.steps, chunk)
+    log(f"timing {args.steps} steps in {len(gs)} graphs")
+    dt = gpu.time_graphs(gs)
+    ms_per_step = dt / args.steps * 1e3
+    value = step_bytes * args.steps / dt / 1e9
+
+    log("dominant kernel timing")
+    pair_s = kernel_avg(gpu, gemv_pair)
+    up_s = kernel_avg(gpu, gemv_up)
+    down_s = kernel_avg(gpu, gemv_down)
+    up_b = gemm_bytes(4, 8, 8192, 2048)
+    down_b = gemm_bytes(4, 8, 2048, 8192)
+    pair_b = up_b + down_b
+    roof = {"bound": "hbm", "achieved": pair_b / pair_s / 1e9, "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s", "frac": pair_b / pair_s / HBM_PEAK, "traffic": read_traffic(),
+            "kernel": "decode_kernel<4,1,8>: the step's GEMM launch (int4 skinny GEMM, "
+                      "up N=8192 K=2048 and down N=2048 K=8192 in one launch, M=8)",
+            "algorithmic_bytes_per_launch": pair_b, "us_per_launch": pair_s * 1e6,
+            "timing": "HIP events around a graph of 48 back-to-back launches / 48",
+            "single_shape_launches": {
+                "up": {"us": up_s * 1e6, "GB_s": up_b / up_s / 1e9, "frac": up_b / up_s / HBM_PEAK},
+                "down": {"us": down_s * 1e6, "GB_s": down_b / down_s / 1e9,
+                         "frac": down_b / down_s / HBM_PEAK}}}
+
+    extra = {}
+    if not args.no_extra:
+        for name, fn in (("cfg1", extra_cfg1), ("cfg3", extra_cfg3), ("cfg5", extra_cfg5),
+                         ("cfg4", extra_cfg4)):
+            log("extra", name)
+            try:
+                extra[name] = fn(gpu)
+            except Exception as e:  # report, keep the headline line
+                extra[name] = {"error": repr(e)}
+            gpu.t.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        try:
+            cpu = cpu_baseline(host, args.cpu_seconds)
+        except Exception as e:
+            cpu = {"error": repr(e)}
+
+    out = {
+        "metric": "decode GEMV HBM GB/s (M=8 int4 g64, up+down, incl. quantise+pack)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (device-generated: N(0,1) activations, uniform int4/int8 weights, "
+                "uniform scales; 48 rotating weight copies)",
+        "config": {"workload": "BASELINE configs[1]: batched decode skinny GEMM M=8, int4 g64, "
+                               "up N=8192 K=2048 + down N=2048 K=8192",
+                   "global_batch": 8, "algorithmic_bytes_per_step": step_bytes,
+                   "frac_hbm_step": value * 1e9 / HBM_PEAK},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -64,7 +64,9 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_prep_rows_hip.argtypes = [p, i, p, p, p, p, i, i, i, i, i]
     L.fgm_quant_act_hip.argtypes = [p, i, i, p, p]
     L.fgm_fwht_hip.argtypes = [p, i, i]
-    for name in ("fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
+    L.fgm_hip_gemm_batch_dev.argtypes = [p, i, p]
+    L.fgm_hip_prep_batch_dev.argtypes = [p, i, p]
+    for name in ("fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
                  "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path"):
         getattr(L, name).restype = i
@@ -77,5 +79,22 @@ def check(status: int) -> None:
         raise FgmHipError(f"status {status}: {lib().fgm_hip_last_error().decode()}")
 
 
+class GemmDesc(_C.Structure):
+    """fgm_hip_gemm_desc (include/fgm_hip.h)."""
+    _fields_ = [("bits", _C.c_int), ("m", _C.c_int), ("n", _C.c_int), ("k", _C.c_int),
+                ("group", _C.c_int), ("a", _C.c_void_p), ("a_scale", _C.c_void_p),
+                ("b", _C.c_void_p), ("b_scale", _C.c_void_p), ("c", _C.c_void_p),
+                ("ldc", _C.c_int), ("n0", _C.c_int), ("n1", _C.c_int)]
+
+
+class PrepDesc(_C.Structure):
+    """fgm_hip_prep_desc (include/fgm_hip.h)."""
+    _fields_ = [("src", _C.c_void_p), ("lda", _C.c_int), ("rot", _C.c_void_p),
+                ("qa", _C.c_void_p), ("qs", _C.c_void_p), ("pa", _C.c_void_p),
+                ("m", _C.c_int), ("k", _C.c_int), ("hsz", _C.c_int), ("r0", _C.c_int),
+                ("r1", _C.c_int)]
+
+
 from .kernels import (  # noqa: E402,F401
-    Backend, backend, fwht, gemm_q4g, gemm_q8c, pack_a, packed_a_len, prep_rows, quant_act)
+    Backend, backend, fwht, gemm_batch, gemm_q4g, gemm_q8c, pack_a, packed_a_len, prep_batch,
+    prep_rows, quant_act)

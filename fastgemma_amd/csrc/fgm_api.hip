@@ -70,7 +70,6 @@ int ensure_device() {
   return FGM_HIP_OK;
 }
 
-constexpr size_t LDS_LIMIT = 160 * 1024;
 // One activation row (f32) is staged whole in LDS by the preamble kernels.
 constexpr size_t ROW_LDS_LIMIT = 128 * 1024;
 
@@ -92,26 +91,70 @@ int check_gemm(int m, int n, int k, int ldc, int n0, int n1, int bits, int group
 
 // Skinny kernel for m <= 64 when its LDS fits, else the dense MFMA kernel.
 int gemm_path(int bits, int m, int k, int group) {
-  if (m > 64) return 1;
-  if (bits == 4 && fgm_decode_lds_bytes(4, m, k, group) > LDS_LIMIT) return 1;
-  return 0;
+  return fgm_decode_fits(bits, m, k, group) ? 0 : 1;
+}
+
+GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, const void* b,
+                   const void* b_scale, int group, float* c, int ldc, int n0, int n1,
+                   int32_t* acc, int ldacc) {
+  GemmProb p;
+  p.A = a;
+  p.a_scale = a_scale;
+  p.B = b;
+  p.b_scale = b_scale;
+  p.C = c;
+  p.acc_out = acc;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.group = group;
+  p.ldc = ldc;
+  p.ldacc = ldacc;
+  p.n0 = n0;
+  p.nblocks = n1 - n0;
+  p.wg0 = 0;
+  return p;
+}
+
+// Launch validated problems of one weight type: skinny ones share launches,
+// dense ones share launches, FGM_MAX_BATCH per launch.  Empty problems are
+// skipped; an empty contraction (k == 0) writes 0, as the reference does.
+int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
+  GemmBatch sk{}, de{};
+  auto flush = [&](GemmBatch& b, int dense) -> int {
+    if (!b.count) return FGM_HIP_OK;
+    hipError_t e = dense ? fgm_launch_gemm(bits, b, st) : fgm_launch_decode(bits, b, st);
+    b.count = 0;
+    if (e != hipSuccess) return hip_fail(e, dense ? "dense GEMM launch" : "skinny GEMM launch");
+    return FGM_HIP_OK;
+  };
+  for (int i = 0; i < count; i++) {
+    const GemmProb& p = probs[i];
+    if (p.M == 0 || p.nblocks == 0) continue;
+    if (p.K == 0) {
+      if (!p.acc_out)
+        HIPCHK(hipMemset2DAsync(p.C + 16 * p.n0, (size_t)p.ldc * 4, 0, (size_t)p.nblocks * 64,
+                                p.M, st));
+      continue;
+    }
+    const int dense = gemm_path(bits, p.M, p.K, p.group);
+    GemmBatch& b = dense ? de : sk;
+    b.p[b.count++] = p;
+    if (b.count == FGM_MAX_BATCH) {
+      int rc = flush(b, dense);
+      if (rc) return rc;
+    }
+  }
+  int rc = flush(sk, 0);
+  if (rc) return rc;
+  return flush(de, 1);
 }
 
 int run_gemm(int bits, int m, int n, int k, const int8_t* a, const float* a_scale, const void* b,
              const void* b_scale, int group, float* c, int ldc, int n0, int n1, int32_t* acc,
              int ldacc, hipStream_t st) {
-  if (m == 0 || n1 == n0 || k == 0) {
-    if (k == 0 && m > 0 && n1 > n0 && !acc) {
-      // empty contraction: the reference writes 0 * scales = 0
-      HIPCHK(hipMemset2DAsync(c + 16 * n0, (size_t)ldc * 4, 0, (size_t)(n1 - n0) * 64, m, st));
-    }
-    return FGM_HIP_OK;
-  }
-  GemmArgs ga{m, n, k, a, a_scale, b, b_scale, group, c, ldc, n0, acc, ldacc};
-  hipError_t e = gemm_path(bits, m, k, group) == 0 ? fgm_launch_decode(bits, ga, n1 - n0, st)
-                                                   : fgm_launch_gemm(bits, ga, n1 - n0, st);
-  if (e != hipSuccess) return hip_fail(e, "GEMM launch");
-  return FGM_HIP_OK;
+  GemmProb p = make_prob(m, n, k, a, a_scale, b, b_scale, group, c, ldc, n0, n1, acc, ldacc);
+  return run_probs(bits, &p, 1, st);
 }
 
 float fwht_scale(int hsz) { return hsz > 0 ? 1.0f / sqrtf((float)hsz) : 1.0f; }
@@ -242,6 +285,25 @@ int dropin_gemm(int bits, int m, int n, int k, const int8_t* a, const float* a_s
   return FGM_HIP_OK;
 }
 
+int check_prep(const fgm_hip_prep_desc& d) {
+  const int m = d.m, k = d.k, hsz = d.hsz, r0 = d.r0, r1 = d.r1, lda = d.lda;
+  if (r0 >= r1) return FGM_HIP_OK;
+  if (k <= 0 || k % 64) return fail(FGM_HIP_EINVAL, "prep_rows: k=%d must be a positive multiple of 64", k);
+  if (r0 < 0 || r0 % 16) return fail(FGM_HIP_EINVAL, "prep_rows: r0=%d must be a multiple of 16", r0);
+  if (r1 > m) return fail(FGM_HIP_EINVAL, "prep_rows: r1=%d > m=%d", r1, m);
+  if (lda < k) return fail(FGM_HIP_EINVAL, "prep_rows: lda=%d < k=%d", lda, k);
+  if (hsz < 0 || (hsz > 0 && (!pow2(hsz) || k % hsz)))
+    return fail(FGM_HIP_EINVAL, "prep_rows: hsz=%d must be 0 or a power of two dividing k=%d", hsz, k);
+  if ((size_t)k * 4 > ROW_LDS_LIMIT)
+    return fail(FGM_HIP_EINVAL, "prep_rows: k=%d > 32768 (one row must fit in LDS)", k);
+  if (!d.src || !d.qs || !d.pa) return fail(FGM_HIP_EINVAL, "prep_rows: src, qs and pa are required");
+  const int blk_end = ((r1 + 15) / 16) * 16;
+  if (r1 < m && blk_end > r1 && !d.qa)
+    return fail(FGM_HIP_EINVAL, "prep_rows: rows [%d,%d) are packed from qa, which is NULL", r1,
+                blk_end < m ? blk_end : m);
+  return FGM_HIP_OK;
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -299,24 +361,63 @@ int fgm_hip_acc_q4g_dev(int m, int n, int k, const int8_t* a, const uint8_t* bq,
 
 int fgm_hip_prep_rows_dev(const float* src, int lda, float* rot, int8_t* qa, float* qs,
                           int8_t* pa, int m, int k, int hsz, int r0, int r1, void* stream) {
-  if (r0 >= r1) return FGM_HIP_OK;
-  if (k <= 0 || k % 64) return fail(FGM_HIP_EINVAL, "prep_rows: k=%d must be a positive multiple of 64", k);
-  if (r0 < 0 || r0 % 16) return fail(FGM_HIP_EINVAL, "prep_rows: r0=%d must be a multiple of 16", r0);
-  if (r1 > m) return fail(FGM_HIP_EINVAL, "prep_rows: r1=%d > m=%d", r1, m);
-  if (lda < k) return fail(FGM_HIP_EINVAL, "prep_rows: lda=%d < k=%d", lda, k);
-  if (hsz < 0 || (hsz > 0 && (!pow2(hsz) || k % hsz)))
-    return fail(FGM_HIP_EINVAL, "prep_rows: hsz=%d must be 0 or a power of two dividing k=%d", hsz, k);
-  if ((size_t)k * 4 > ROW_LDS_LIMIT) return fail(FGM_HIP_EINVAL, "prep_rows: k=%d > 32768 (one row must fit in LDS)", k);
-  if (!src || !qs || !pa) return fail(FGM_HIP_EINVAL, "prep_rows: src, qs and pa are required");
-  const int blk_end = ((r1 + 15) / 16) * 16;
-  if (r1 < m && blk_end > r1 && !qa)
-    return fail(FGM_HIP_EINVAL, "prep_rows: rows [%d,%d) are packed from qa, which is NULL", r1,
-                blk_end < m ? blk_end : m);
+  fgm_hip_prep_desc d{src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1};
+  return fgm_hip_prep_batch_dev(&d, 1, stream);
+}
+
+int fgm_hip_prep_batch_dev(const fgm_hip_prep_desc* d, int count, void* stream) {
+  if (count < 0 || (count > 0 && !d)) return fail(FGM_HIP_EINVAL, "prep batch: bad descriptor array");
+  for (int i = 0; i < count; i++) {
+    int rc = check_prep(d[i]);
+    if (rc) return rc;
+  }
   int rc = ensure_device();
   if (rc) return rc;
-  hipError_t e = fgm_launch_prep_rows(src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1,
-                                      fwht_scale(hsz), (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "prep_rows launch");
+  PrepBatch b{};
+  for (int i = 0; i < count; i++) {
+    const fgm_hip_prep_desc& x = d[i];
+    if (x.r0 >= x.r1) continue;
+    b.p[b.count++] = PrepProb{x.src, x.rot, x.qa, x.qs, x.pa, x.lda, x.m, x.k, x.hsz, x.r0, x.r1,
+                              fwht_scale(x.hsz), 0};
+    if (b.count == FGM_MAX_BATCH || i == count - 1) {
+      hipError_t e = fgm_launch_prep(b, (hipStream_t)stream);
+      if (e != hipSuccess) return hip_fail(e, "prep launch");
+      b.count = 0;
+    }
+  }
+  if (b.count) {
+    hipError_t e = fgm_launch_prep(b, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+  }
+  return FGM_HIP_OK;
+}
+
+int fgm_hip_gemm_batch_dev(const fgm_hip_gemm_desc* d, int count, void* stream) {
+  if (count < 0 || (count > 0 && !d)) return fail(FGM_HIP_EINVAL, "gemm batch: bad descriptor array");
+  for (int i = 0; i < count; i++) {
+    const fgm_hip_gemm_desc& x = d[i];
+    if (x.bits != 4 && x.bits != 8) return fail(FGM_HIP_EINVAL, "gemm batch[%d]: bits=%d", i, x.bits);
+    int rc = check_gemm(x.m, x.n, x.k, x.ldc, x.n0, x.n1, x.bits, x.group);
+    if (rc) return rc;
+  }
+  int rc = ensure_device();
+  if (rc) return rc;
+  GemmProb p4[64], p8[64];
+  int n4 = 0, n8 = 0;
+  for (int i = 0; i < count; i++) {
+    const fgm_hip_gemm_desc& x = d[i];
+    GemmProb p = make_prob(x.m, x.n, x.k, x.a, x.a_scale, x.b, x.b_scale, x.group, x.c, x.ldc,
+                           x.n0, x.n1, nullptr, 0);
+    GemmProb* dst = x.bits == 4 ? p4 : p8;
+    int& n = x.bits == 4 ? n4 : n8;
+    dst[n++] = p;
+    if (n == 64) {
+      if ((rc = run_probs(x.bits, dst, n, (hipStream_t)stream))) return rc;
+      n = 0;
+    }
+  }
+  if (n4 && (rc = run_probs(4, p4, n4, (hipStream_t)stream))) return rc;
+  if (n8 && (rc = run_probs(8, p8, n8, (hipStream_t)stream))) return rc;
   return FGM_HIP_OK;
 }
 
@@ -325,8 +426,10 @@ int fgm_hip_quant_act_dev(const float* x, int rows, int k, int8_t* q, float* sca
   if ((size_t)k * 4 > ROW_LDS_LIMIT) return fail(FGM_HIP_EINVAL, "quant_act: k=%d > 32768 (one row must fit in LDS)", k);
   int rc = ensure_device();
   if (rc) return rc;
-  hipError_t e = fgm_launch_prep_rows(x, k, nullptr, q, scale, nullptr, rows, k, 0, 0, rows, 1.0f,
-                                      (hipStream_t)stream);
+  PrepBatch b{};
+  b.p[0] = PrepProb{x, nullptr, q, scale, nullptr, k, rows, k, 0, 0, rows, 1.0f, 0};
+  b.count = 1;
+  hipError_t e = fgm_launch_prep(b, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "quant_act launch");
   return FGM_HIP_OK;
 }

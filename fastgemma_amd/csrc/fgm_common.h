@@ -65,3 +65,30 @@ FGM_DEV int8_t quant_tail(float v) {
   int32_t iv = (int32_t)(uint32_t)(uint64_t)l;
   return (int8_t)(iv > 127 ? 127 : (iv < -127 ? -127 : iv));
 }
+
+// Raw buffer access (gfx9 buffer descriptor, no stride).  A lane whose byte
+// offset lies at or beyond `bytes` reads 0 without touching memory, which is
+// how the kernels mask rows and columns without branches.
+constexpr int FGM_BUF_FLAGS = 0x00020000;  // gfx9 family descriptor word 3
+constexpr uint32_t FGM_OOB = 0x80000000u;  // an offset no buffer here reaches
+
+FGM_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           FGM_BUF_FLAGS);
+}
+
+FGM_DEV int32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+FGM_DEV v4i buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
+FGM_DEV uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// threadIdx.x / 64 as a scalar: lets the compiler keep per-wave loop bounds
+// and tile indices in SGPRs and branch uniformly.
+FGM_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }

@@ -6,29 +6,51 @@
 #include <stddef.h>
 #include <stdint.h>
 
-struct GemmArgs {
-  int M, N, K;
+// Independent problems served by one launch.
+constexpr int FGM_MAX_BATCH = 4;
+
+struct GemmProb {
   const int8_t* A;        // packed A [ceil(M/16)][K/64][16][64]
   const float* a_scale;   // [M]
   const void* B;          // int8 tiles, or packed int4 tiles
   const void* b_scale;    // f32 [N] (q8c) or f16 bits [K/group][N] (q4g)
-  int group;              // q4g only
   float* C;
-  int ldc;
-  int n0;                 // first n-block; blockIdx enumerates [n0, n1)
   int32_t* acc_out;       // raw int32 accumulators instead of C when non-null
-  int ldacc;
+  int M, N, K, group, ldc, ldacc;
+  int n0, nblocks;        // n-block range [n0, n0 + nblocks)
+  int wg0;                // first workgroup of this problem (set by the launcher)
 };
 
-hipError_t fgm_launch_prep_rows(const float* src, int lda, float* rot, int8_t* qa, float* qs,
-                                int8_t* pa, int m, int k, int hsz, int r0, int r1,
-                                float fwht_scale, hipStream_t st);
+struct GemmBatch {
+  GemmProb p[FGM_MAX_BATCH];
+  int count;
+};
+
+struct PrepProb {
+  const float* src;
+  float* rot;      // may be null (device API only)
+  int8_t* qa;      // may be null (device API only)
+  float* qs;
+  int8_t* pa;      // null for quant_act
+  int lda, m, k, hsz, r0, r1;
+  float fwht_scale;
+  int wg0;         // first workgroup (set by the launcher)
+};
+
+struct PrepBatch {
+  PrepProb p[FGM_MAX_BATCH];
+  int count;
+};
+
+hipError_t fgm_launch_prep(const PrepBatch& b, hipStream_t st);
 hipError_t fgm_launch_pack_a(int M, int K, const int8_t* A, int8_t* Ap, hipStream_t st);
 hipError_t fgm_launch_fwht(float* x, int n, int hsz, float scale, hipStream_t st);
 
-// Skinny path, M <= 64.  nblocks = n1 - n0 workgroups.
-hipError_t fgm_launch_decode(int bits, const GemmArgs& a, int nblocks, hipStream_t st);
+// Skinny weight-stream path, M <= 64 (all problems of a batch share the
+// weight type and are served by one launch).
+bool fgm_decode_fits(int bits, int M, int K, int group);
 size_t fgm_decode_lds_bytes(int bits, int M, int K, int group);
+hipError_t fgm_launch_decode(int bits, const GemmBatch& b, hipStream_t st);
 
 // Dense MFMA path (any M).
-hipError_t fgm_launch_gemm(int bits, const GemmArgs& a, int nblocks, hipStream_t st);
+hipError_t fgm_launch_gemm(int bits, const GemmBatch& b, hipStream_t st);

@@ -8,6 +8,7 @@
 // maximum (order-free for non-NaN rows), then quantised and written to the
 // row-major int8 copy and to its slots in the packed tiles.
 #include "fgm_common.h"
+#include "fgm_kernels.h"
 
 namespace {
 
@@ -50,22 +51,22 @@ __device__ __forceinline__ size_t pa_off(int row, int col, int KB) {
   return (((size_t)(row >> 4) * KB + (col >> 6)) * 16 + (row & 15)) * 64 + (col & 63);
 }
 
-struct PrepArgs {
-  const float* src;
-  int lda;
-  float* rot;      // may be null (device API only)
-  int8_t* qa;      // may be null (device API only)
-  float* qs;
-  int8_t* pa;      // may be null when k % 64 != 0 (quant_act)
-  int m, k, hsz, r0, r1;
-  int row_begin;   // first row this launch covers (blockIdx.x == 0)
-  float fwht_scale;
-};
+// The problem a workgroup belongs to, chosen with uniform selects so the
+// kernel-argument array is never indexed dynamically.
+__device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
+  const int b = blockIdx.x;
+  PrepProb p = bt.p[0];
+  if (bt.count > 1 && b >= bt.p[1].wg0) p = bt.p[1];
+  if (bt.count > 2 && b >= bt.p[2].wg0) p = bt.p[2];
+  if (bt.count > 3 && b >= bt.p[3].wg0) p = bt.p[3];
+  return p;
+}
 
-__global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
+__global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
   __shared__ float red[PREP_THREADS / 64];
-  const int row = a.row_begin + blockIdx.x;
+  const PrepProb a = pick(bt);
+  const int row = a.r0 + (blockIdx.x - a.wg0);
   const int k = a.k, KB = k >> 6;
 
   if (row >= a.r1) {
@@ -84,8 +85,40 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
     return;
   }
 
+  // Stage the row in LDS: eight loads in flight per thread before any store.
+  // Lanes past the row's end read 0 through the buffer range check.
   const float* src = a.src + (size_t)row * a.lda;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) buf[i] = src[i];
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)k * 4);
+  if ((((uintptr_t)src) & 15) == 0 && (k & 3) == 0) {
+    const int k4 = k >> 2;
+    for (int base = 0; base < k4; base += PREP_THREADS * 8) {
+      v4i v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
+        v[u] = buf_load_b128(rs, c < k4 ? (uint32_t)c * 16 : FGM_OOB, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
+        if (c < k4) *(v4i*)(buf + 4 * c) = v[u];
+      }
+    }
+  } else {
+    for (int base = 0; base < k; base += PREP_THREADS * 8) {
+      int32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
+        v[u] = buf_load_b32(rs, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
+        if (c < k) buf[c] = __int_as_float(v[u]);
+      }
+    }
+  }
   __syncthreads();
   if (a.hsz > 0) fwht_lds(buf, k, a.hsz, a.fwht_scale);
 
@@ -162,17 +195,24 @@ static hipError_t allow_big_lds(K kernel) {
                              160 * 1024 - 1024);
 }
 
-hipError_t fgm_launch_prep_rows(const float* src, int lda, float* rot, int8_t* qa, float* qs,
-                                int8_t* pa, int m, int k, int hsz, int r0, int r1,
-                                float fwht_scale, hipStream_t st) {
-  if (r0 >= r1) return hipSuccess;
+hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
   static hipError_t attr = allow_big_lds(prep_rows_kernel);
   if (attr != hipSuccess) return attr;
-  PrepArgs a{src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1, r0, fwht_scale};
-  // rows [r0, r1) compute; rows [r1, end of r1's tile block) only pack
-  int end = pa ? ((r1 + 15) / 16) * 16 : r1;
-  hipLaunchKernelGGL(prep_rows_kernel, dim3(end - r0), dim3(PREP_THREADS),
-                     (size_t)k * sizeof(float), st, a);
+  PrepBatch b = in;
+  int nwg = 0, kmax = 0;
+  for (int i = 0; i < b.count; i++) {
+    PrepProb& p = b.p[i];
+    p.wg0 = nwg;
+    if (p.r0 < p.r1) {
+      // rows [r0, r1) compute; rows [r1, end of r1's tile block) only pack
+      const int end = p.pa ? ((p.r1 + 15) / 16) * 16 : p.r1;
+      nwg += end - p.r0;
+    }
+    if (p.k > kmax) kmax = p.k;
+  }
+  if (nwg == 0) return hipSuccess;
+  hipLaunchKernelGGL(prep_rows_kernel, dim3(nwg), dim3(PREP_THREADS), (size_t)kmax * sizeof(float),
+                     st, b);
   return hipGetLastError();
 }
 

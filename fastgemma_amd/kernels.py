@@ -178,6 +178,41 @@ def acc_q4g(m, n, k, a, bq, group, acc, ldacc, n0, n1) -> None:
                                     _stream()))
 
 
+def _ptr_or_none(t):
+    return None if t is None else _dp(t)
+
+
+def gemm_batch(problems, stream=None) -> None:
+    """Several GEMMs on device tensors in as few launches as possible.
+
+    `problems`: iterable of dicts with keys bits (4 or 8), m, n, k, a, a_scale,
+    b, b_scale, c, ldc, n0, n1 and, for bits == 4, group."""
+    from . import GemmDesc
+    probs = list(problems)
+    arr = (GemmDesc * max(1, len(probs)))()
+    for i, p in enumerate(probs):
+        assert p["k"] % 64 == 0 and p["n"] % 16 == 0
+        assert (p["n1"] - p["n0"]) % 4 == 0, "n-block range must be a multiple of 4"
+        arr[i] = GemmDesc(p["bits"], p["m"], p["n"], p["k"], p.get("group", 64), _dp(p["a"]),
+                          _dp(p["a_scale"]), _dp(p["b"]), _dp(p["b_scale"]), _dp(p["c"]),
+                          p["ldc"], p["n0"], p["n1"])
+    check(lib().fgm_hip_gemm_batch_dev(arr, len(probs), _stream() if stream is None else stream))
+
+
+def prep_batch(problems, stream=None) -> None:
+    """fgm_prep_rows for several device activations in one launch.  Each dict:
+    src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1 (rot / qa may be None)."""
+    from . import PrepDesc
+    probs = list(problems)
+    arr = (PrepDesc * max(1, len(probs)))()
+    for i, p in enumerate(probs):
+        assert p["r0"] % 16 == 0, "prep row start must be tile-aligned"
+        arr[i] = PrepDesc(_dp(p["src"]), p["lda"], _ptr_or_none(p.get("rot")),
+                          _ptr_or_none(p.get("qa")), _dp(p["qs"]), _dp(p["pa"]), p["m"], p["k"],
+                          p.get("hsz", 0), p["r0"], p["r1"])
+    check(lib().fgm_hip_prep_batch_dev(arr, len(probs), _stream() if stream is None else stream))
+
+
 def gemm_path(bits: int, m: int, k: int, group: int = 64) -> str:
     """'skinny' or 'dense': which kernel family serves this shape."""
     return ("skinny", "dense")[lib().fgm_hip_gemm_path(bits, m, k, group)]

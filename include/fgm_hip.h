@@ -33,8 +33,9 @@
  * Preconditions (the reference asserts them in debug Rust only,
  * lib.rs:161-163,176-177,201-202,521; they are always checked here):
  *   K % 64 == 0, N % 16 == 0, 0 <= n0 <= n1 <= N/16, (n1 - n0) % 4 == 0,
- *   ldc >= N... (ldc >= 16*n1), q4g: group % 64 == 0 and K % group == 0,
- *   prep_rows: r0 % 16 == 0, k % 64 == 0; fwht: hsz a power of two, n % hsz == 0.
+ *   ldc >= 16*n1, q4g: group % 64 == 0 and K % group == 0,
+ *   prep_rows: r0 % 16 == 0, k % 64 == 0, k <= 32768 (a row is staged in LDS);
+ *   fwht: hsz a power of two, n % hsz == 0.
  */
 #ifndef FGM_HIP_H
 #define FGM_HIP_H
@@ -128,6 +129,39 @@ int fgm_hip_fwht_dev(float *x, int n, int hsz, void *stream);
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);
+
+/* ------------------------------------------------------------ batched calls
+ * No single reference counterpart: one call for the GEMMs a forward pass
+ * issues back to back on the same activation (q/k/v, gate/up: forward.rs:
+ * 484,499-500,619-622) or on independent ones.  Up to four GEMMs of one
+ * weight type share a launch; the results equal the one-at-a-time calls
+ * byte for byte.  The descriptors are read during the call only. */
+typedef struct fgm_hip_gemm_desc {
+  int bits;               /* 8: q8c (b int8 tiles, b_scale f32 [n]);
+                             4: q4g (b packed int4, b_scale f16 bits [k/group][n]) */
+  int m, n, k, group;     /* group: q4g only */
+  const int8_t *a;        /* packed A (device) */
+  const float *a_scale;
+  const void *b;
+  const void *b_scale;
+  float *c;
+  int ldc, n0, n1;
+} fgm_hip_gemm_desc;
+
+int fgm_hip_gemm_batch_dev(const fgm_hip_gemm_desc *descs, int count, void *stream);
+
+/* fgm_prep_rows for several activations in one launch. */
+typedef struct fgm_hip_prep_desc {
+  const float *src;
+  int lda;
+  float *rot;             /* may be NULL */
+  int8_t *qa;             /* may be NULL unless rows of r1's tile block lie in [r1, m) */
+  float *qs;
+  int8_t *pa;
+  int m, k, hsz, r0, r1;
+} fgm_hip_prep_desc;
+
+int fgm_hip_prep_batch_dev(const fgm_hip_prep_desc *descs, int count, void *stream);
 
 #ifdef __cplusplus
 }

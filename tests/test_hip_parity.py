@@ -261,3 +261,47 @@ def test_gpu_vs_reference_live(kind, M):
     else:
         R.fgm_gemm_q4g_vnni(M, N, Kd, P(Ap), P(a_s), P(B), P(bs), 64, P(RC), N, 0, N // 16)
     assert _bits_equal(C, RC)
+
+
+# ----------------------------------------------------------- batched calls
+@pytest.mark.parametrize("M", [8, 256])
+def test_batched_gemms_equal_single_calls(M):
+    """One batched call (several GEMMs per launch, both weight types, mixed
+    shapes) writes the same bytes as the single calls."""
+    from fastgemma_amd import kernels
+    t = H.torch()
+    specs = [("q4g", 8192 // 4, 2048), ("q4g", 2048 // 4, 8192 // 2), ("q8c", 512, 2048),
+             ("q4g", 512, 2048), ("q8c", 1024, 1024), ("q4g", 256, 1024)]
+    probs, refs = [], []
+    for i, (kind, N, Kd) in enumerate(specs):
+        A, Ap, a_s, B, bs = _inputs(kind, M, N, Kd, 64, seed=7000 + i)
+        C = t.full((M, N), 9.0, device="cuda")
+        probs.append(dict(bits=8 if kind == "q8c" else 4, m=M, n=N, k=Kd, group=64,
+                          a=H.dev(Ap), a_scale=H.dev(a_s), b=H.dev(B), b_scale=H.dev(bs), c=C,
+                          ldc=N, n0=0, n1=N // 16))
+        refs.append(H.gpu_gemm(kind, M, N, Kd, Ap, a_s, B, bs, 64, fill=9.0))
+    kernels.gemm_batch(probs)
+    for p, r in zip(probs, refs):
+        assert _bits_equal(H.host(p["c"]), r)
+
+
+def test_batched_prep_equals_single_calls():
+    from fastgemma_amd import kernels
+    t = H.torch()
+    probs, refs = [], []
+    for i, (m, k, hsz) in enumerate([(8, 2048, 0), (8, 8192, 0), (37, 256, 128), (256, 2048, 0),
+                                     (1, 1024, 64)]):
+        x = oracle.gen_normal(60 + i, m * k).reshape(m, k)
+        qs = t.zeros(m, device="cuda")
+        pa = t.zeros(oracle.packed_a_len(m, k), dtype=t.int8, device="cuda")
+        qa = t.zeros((m, k), dtype=t.int8, device="cuda")
+        probs.append(dict(src=H.dev(x), lda=k, rot=None, qa=qa, qs=qs, pa=pa, m=m, k=k, hsz=hsz,
+                          r0=0, r1=m))
+        xr = oracle.fwht(x, hsz) if hsz else x
+        rq, rs = oracle.quant_act(xr, m, k)
+        refs.append((rq, rs, oracle.pack_a(m, k, rq)))
+    kernels.prep_batch(probs)
+    for p, (rq, rs, rap) in zip(probs, refs):
+        assert np.array_equal(H.host(p["qa"]), rq)
+        assert _bits_equal(H.host(p["qs"]), rs)
+        assert np.array_equal(H.host(p["pa"]), rap)
