@@ -113,6 +113,7 @@ GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, c
   p.n0 = n0;
   p.nblocks = n1 - n0;
   p.wg0 = 0;
+  p.tw = p.ks = p.nbw = 0;
   return p;
 }
 

@@ -58,6 +58,19 @@ FGM_DEV int8_t quant_vec(float v) {
   return (int8_t)(int)r;
 }
 
+// quant_vec without branches, as an int in [-128, 127].
+FGM_DEV int quant_vec_i(float v) {
+  const int q = (int)__builtin_amdgcn_fmed3f(__builtin_rintf(v), -128.0f, 127.0f);
+  return __builtin_fabsf(v) < 2147483648.0f ? q : -128;
+}
+
+// the low bytes of four ints, q0 in bits 7..0
+FGM_DEV uint32_t pack4_i8(int q0, int q1, int q2, int q3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0C0C0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x04000C0Cu);
+  return lo | hi;
+}
+
 FGM_DEV int8_t quant_tail(float v) {
   int64_t l;
   if (!(__builtin_fabsf(v) < 9223372036854775808.0f)) l = INT64_MIN;

@@ -19,6 +19,8 @@ struct GemmProb {
   int M, N, K, group, ldc, ldacc;
   int n0, nblocks;        // n-block range [n0, n0 + nblocks)
   int wg0;                // first workgroup of this problem (set by the launcher)
+  int tw, ks, nbw;        // skinny path: k-blocks per wave, waves per n-block,
+                          // n-blocks per workgroup (set by the launcher)
 };
 
 struct GemmBatch {

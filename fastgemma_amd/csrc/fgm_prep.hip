@@ -2,38 +2,31 @@
 // quantisation and A tile-packing -- the device side of fgm_prep_rows,
 // fgm_quant_act, fgm_fwht and fgm_pack_a (ops.c:153-204, 279-314).
 //
-// One workgroup owns one activation row.  The row is staged in LDS, rotated
-// there (every FWHT stage is one add or one subtract per element, so the
-// parallel schedule gives the reference's bytes), reduced to its absolute
-// maximum (order-free for non-NaN rows), then quantised and written to the
-// row-major int8 copy and to its slots in the packed tiles.
+// One workgroup owns one activation row; each thread holds up to VMAX
+// consecutive float4s of it (vector i = thread + v * blockDim covers columns
+// 4i..4i+3) in registers from load to store.  With a rotation the row goes
+// through LDS once (every FWHT stage is one add or one subtract per element,
+// so the parallel schedule gives the reference's bytes).  The absolute
+// maximum is a wave reduction plus one LDS exchange (order-free for non-NaN
+// rows); then each float4 becomes one dword of the row-major int8 copy and
+// one dword of its packed tile.
 #include "fgm_common.h"
 #include "fgm_kernels.h"
 
 namespace {
 
-constexpr int PREP_THREADS = 256;
+constexpr int PREP_MAX_THREADS = 1024;
+constexpr int VMAX = 8;  // float4s per thread: rows up to 8 * 4 * 1024 = 32768 floats
 
-// Block-wide max of non-negative floats.
-__device__ float block_max(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float m = red[0];
-  for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = fmaxf(m, red[w]);
-  __syncthreads();
-  return m;
-}
-
-// In-place normalised FWHT of the `k` floats in LDS, blocks of `hsz`
-// (ops.c:153-175).  `scale` = 1/sqrtf(hsz) computed on the host; it is only
-// applied for hsz >= 16, matching the reference's 16-wide scale loop.
+// In-place normalised FWHT of the `k` floats in LDS, blocks of `hsz` (a power
+// of two; ops.c:153-175).  `scale` = 1/sqrtf(hsz) computed on the host; it is
+// only applied for hsz >= 16, matching the reference's 16-wide scale loop.
 __device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
   const int half = k >> 1;
-  for (int len = 1; len < hsz; len <<= 1) {
+  for (int lg = 0; (1 << lg) < hsz; lg++) {
+    const int len = 1 << lg;
     for (int p = threadIdx.x; p < half; p += blockDim.x) {
-      const int i = (p / len) * (len << 1) + (p % len);  // pairs never straddle a block
+      const int i = ((p >> lg) << (lg + 1)) | (p & (len - 1));  // pairs never straddle a block
       const float u = buf[i], v = buf[i + len];
       buf[i] = u + v;
       buf[i + len] = u - v;
@@ -44,6 +37,24 @@ __device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
     for (int i = threadIdx.x; i < k; i += blockDim.x) buf[i] = buf[i] * scale;
     __syncthreads();
   }
+}
+
+// Maximum over the 64 lanes of a wave: DPP within each 16-lane row, then the
+// four row results read back as scalars.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = dpp_max<0xB1>(v);   // quad_perm 1,0,3,2
+  v = dpp_max<0x4E>(v);   // quad_perm 2,3,0,1
+  v = dpp_max<0x124>(v);  // row_ror 4
+  v = dpp_max<0x128>(v);  // row_ror 8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // Packed-A byte offset of (row, col): [row/16][col/64][row%16][col%64].
@@ -62,18 +73,19 @@ __device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
   return p;
 }
 
-__global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepBatch bt) {
+__global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
-  __shared__ float red[PREP_THREADS / 64];
+  __shared__ float red[PREP_MAX_THREADS / 64];
   const PrepProb a = pick(bt);
   const int row = a.r0 + (blockIdx.x - a.wg0);
   const int k = a.k, KB = k >> 6;
+  const int T = blockDim.x, tid = threadIdx.x;
 
   if (row >= a.r1) {
     // Rows of the last covered tile block beyond r1: zero padding when past m,
     // otherwise whatever the caller's qa row holds (ops.c:308-311).
     if (!a.pa) return;
-    for (int c = threadIdx.x * 4; c < k; c += blockDim.x * 4) {
+    for (int c = tid * 4; c < k; c += T * 4) {
       int32_t v = 0;
       if (row < a.m) {
         const int8_t* q = a.qa + (size_t)row * k + c;
@@ -85,63 +97,96 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepBatch bt) {
     return;
   }
 
-  // Stage the row in LDS: eight loads in flight per thread before any store.
-  // Lanes past the row's end read 0 through the buffer range check.
+  // 1. the row into registers; lanes past its end read 0 (buffer range check)
   const float* src = a.src + (size_t)row * a.lda;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)k * 4);
-  if ((((uintptr_t)src) & 15) == 0 && (k & 3) == 0) {
-    const int k4 = k >> 2;
-    for (int base = 0; base < k4; base += PREP_THREADS * 8) {
-      v4i v[8];
+  const bool vec = ((((uintptr_t)a.src) & 15) == 0) && (a.lda & 3) == 0 && (k & 3) == 0;
+  float x[VMAX][4];
+  if (vec) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
-        v[u] = buf_load_b128(rs, c < k4 ? (uint32_t)c * 16 : FGM_OOB, 0);
-      }
+    for (int v = 0; v < VMAX; v++) {
+      const int c = 4 * (tid + v * T);
+      const v4i q = buf_load_b128(rs, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
-        if (c < k4) *(v4i*)(buf + 4 * c) = v[u];
-      }
+      for (int e = 0; e < 4; e++) x[v][e] = __int_as_float(q[e]);
     }
   } else {
-    for (int base = 0; base < k; base += PREP_THREADS * 8) {
-      int32_t v[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
-        v[u] = buf_load_b32(rs, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
-      }
+    for (int v = 0; v < VMAX; v++) {
+      const int c = 4 * (tid + v * T);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int c = base + (int)threadIdx.x + u * PREP_THREADS;
-        if (c < k) buf[c] = __int_as_float(v[u]);
-      }
+      for (int e = 0; e < 4; e++)
+        x[v][e] = __int_as_float(buf_load_b32(rs, c + e < k ? (uint32_t)(c + e) * 4 : FGM_OOB, 0));
     }
   }
-  __syncthreads();
-  if (a.hsz > 0) fwht_lds(buf, k, a.hsz, a.fwht_scale);
 
+  // 2. optional rotation, through LDS
+  if (a.hsz > 0) {
+#pragma unroll
+    for (int v = 0; v < VMAX; v++) {
+      const int c = 4 * (tid + v * T);
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (c + e < k) buf[c + e] = x[v][e];
+    }
+    __syncthreads();
+    fwht_lds(buf, k, a.hsz, a.fwht_scale);
+#pragma unroll
+    for (int v = 0; v < VMAX; v++) {
+      const int c = 4 * (tid + v * T);
+#pragma unroll
+      for (int e = 0; e < 4; e++) x[v][e] = (c + e < k) ? buf[c + e] : 0.0f;
+    }
+  }
+
+  // 3. absolute maximum of the row
   float mx = 0.0f;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) mx = fmaxf(mx, __builtin_fabsf(buf[i]));
-  mx = block_max(mx, red);
+#pragma unroll
+  for (int v = 0; v < VMAX; v++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) mx = fmaxf(mx, __builtin_fabsf(x[v][e]));
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < (T >> 6); w++) mx = fmaxf(mx, red[w]);
   const float s = (mx == 0.0f) ? 1.0f : mx / 127.0f;
   const float inv = 1.0f / s;
-  if (threadIdx.x == 0) a.qs[row] = s;
+  if (tid == 0) a.qs[row] = s;
 
+  // 4. quantise and store: vector part [0, k & ~15) as _mm512_cvtps_epi32 +
+  //    saturation, the scalar tail as lrintf + clamp (ops.c:194-203)
   const int kv = k & ~15;
   float* rot = a.rot ? a.rot + (size_t)row * k : nullptr;
   int8_t* qa = a.qa ? a.qa + (size_t)row * k : nullptr;
-  // four consecutive columns per thread: one dword store to qa and to pa
-  for (int c = threadIdx.x * 4; c < k; c += blockDim.x * 4) {
-    uint32_t packed = 0;
-    for (int e = 0; e < 4 && c + e < k; e++) {
-      const float x = buf[c + e];
-      if (rot) rot[c + e] = x;
-      const float v = x * inv;
-      const int8_t q = (c + e < kv) ? quant_vec(v) : quant_tail(v);
-      packed |= (uint32_t)(uint8_t)q << (8 * e);
-      if (qa) qa[c + e] = q;
+  const bool dw = (k & 3) == 0;  // rows of qa / rot start 4-byte aligned
+#pragma unroll
+  for (int v = 0; v < VMAX; v++) {
+    const int c = 4 * (tid + v * T);
+    if (c >= k) break;
+    uint32_t packed;
+    if (c + 4 <= kv) {
+      packed = pack4_i8(quant_vec_i(x[v][0] * inv), quant_vec_i(x[v][1] * inv),
+                        quant_vec_i(x[v][2] * inv), quant_vec_i(x[v][3] * inv));
+    } else {
+      packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float y = x[v][e] * inv;
+        const int8_t q = (c + e < kv) ? quant_vec(y) : quant_tail(y);
+        packed |= (uint32_t)(uint8_t)q << (8 * e);
+      }
+    }
+    if (dw && c + 4 <= kv) {
+      if (rot) *(float4*)(rot + c) = make_float4(x[v][0], x[v][1], x[v][2], x[v][3]);
+      if (qa) *(uint32_t*)(qa + c) = packed;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        if (c + e >= k) break;
+        if (rot) rot[c + e] = x[v][e];
+        if (qa) qa[c + e] = (int8_t)(packed >> (8 * e));
+      }
     }
     if (a.pa) *(uint32_t*)(a.pa + pa_off(row, c, KB)) = packed;
   }
@@ -173,7 +218,7 @@ __global__ void pack_a_kernel(int M, int K, const int8_t* __restrict__ A, int8_t
 }
 
 // fgm_fwht on a flat array: one workgroup per `chunk` floats (whole blocks).
-__global__ __launch_bounds__(PREP_THREADS) void fwht_kernel(float* x, int chunk, int hsz,
+__global__ __launch_bounds__(256) void fwht_kernel(float* x, int chunk, int hsz,
                                                             float scale) {
   extern __shared__ float buf[];
   float* p = x + (size_t)blockIdx.x * chunk;
@@ -199,7 +244,7 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
   static hipError_t attr = allow_big_lds(prep_rows_kernel);
   if (attr != hipSuccess) return attr;
   PrepBatch b = in;
-  int nwg = 0, kmax = 0;
+  int nwg = 0, kmax = 0, kfwht = 0;
   for (int i = 0; i < b.count; i++) {
     PrepProb& p = b.p[i];
     p.wg0 = nwg;
@@ -207,12 +252,17 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
       // rows [r0, r1) compute; rows [r1, end of r1's tile block) only pack
       const int end = p.pa ? ((p.r1 + 15) / 16) * 16 : p.r1;
       nwg += end - p.r0;
+      if (p.k > kmax) kmax = p.k;
+      if (p.hsz > 0 && p.k > kfwht) kfwht = p.k;
     }
-    if (p.k > kmax) kmax = p.k;
   }
   if (nwg == 0) return hipSuccess;
-  hipLaunchKernelGGL(prep_rows_kernel, dim3(nwg), dim3(PREP_THREADS), (size_t)kmax * sizeof(float),
-                     st, b);
+  // up to VMAX float4s per thread (fewer waves: a cheaper row reduction),
+  // whole waves, at most 1024 threads
+  int threads = ((kmax + 4 * VMAX - 1) / (4 * VMAX) + 63) / 64 * 64;
+  if (threads < 64) threads = 64;
+  if (threads > PREP_MAX_THREADS) threads = PREP_MAX_THREADS;
+  hipLaunchKernelGGL(prep_rows_kernel, dim3(nwg), dim3(threads), (size_t)kfwht * sizeof(float), st, b);
   return hipGetLastError();
 }
 
@@ -230,7 +280,7 @@ hipError_t fgm_launch_fwht(float* x, int n, int hsz, float scale, hipStream_t st
   if (attr != hipSuccess) return attr;
   int chunk = hsz;
   while (chunk < 2048 && n % (chunk * 2) == 0) chunk *= 2;
-  hipLaunchKernelGGL(fwht_kernel, dim3(n / chunk), dim3(PREP_THREADS),
+  hipLaunchKernelGGL(fwht_kernel, dim3(n / chunk), dim3(256),
                      (size_t)chunk * sizeof(float), st, x, chunk, hsz, scale);
   return hipGetLastError();
 }
