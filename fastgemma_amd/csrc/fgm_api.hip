@@ -132,6 +132,11 @@ int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
   for (int i = 0; i < count; i++) {
     const GemmProb& p = probs[i];
     if (p.M == 0 || p.nblocks == 0) continue;
+    // every operand a launch reads or writes must exist
+    if (!p.acc_out && !p.C) return fail(FGM_HIP_EINVAL, "gemm: c is NULL");
+    if (p.K > 0 && (!p.A || !p.B)) return fail(FGM_HIP_EINVAL, "gemm: a or b is NULL");
+    if (p.K > 0 && !p.acc_out && (!p.a_scale || !p.b_scale))
+      return fail(FGM_HIP_EINVAL, "gemm: a_scale or b_scale is NULL");
     if (p.K == 0) {
       if (!p.acc_out)
         HIPCHK(hipMemset2DAsync(p.C + 16 * p.n0, (size_t)p.ldc * 4, 0, (size_t)p.nblocks * 64,

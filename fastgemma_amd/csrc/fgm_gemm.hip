@@ -2,29 +2,44 @@
 // fgm_gemm_q8c / fgm_gemm_q4g (amx_gemm.c:333-372, 444-475) and their VNNI
 // twins (vnni_gemm.c:224-322).
 //
-// Workgroup tile BM x BN (BN/16 n-blocks), 4 waves in a 2x2 grid, each wave
-// (BM/2) x (BN/2) built from v_mfma_i32_16x16x64_i8, one 64-wide k-block per
-// pipeline stage.  Operands move global -> registers -> LDS:
-//   * a ring of D register stages keeps D k-blocks of loads in flight, so the
-//     L2 / HBM latency is covered by D stages of matrix work;
-//   * LDS is double-buffered, one barrier per k-block;
-//   * A rows are stored as they are, B tiles re-laid column-major (one 64-byte
-//     k-run per column); both with an 80-byte pitch, so every fragment read is
-//     one conflict-free ds_read_b128;
-//   * int4 tiles are sign-extended to int8 on their way into LDS.
-// MFMA k-permutation: operand byte b of lane 16*g + j is k = 16*g + b.
+// Workgroup tile BM x BN, WGM x WGN waves, each wave WMT x WNT tiles of
+// v_mfma_i32_32x32x32_i8 (the i8 MFMA with the highest issue rate on gfx950).
+// One 64-wide k-block per pipeline stage; NS stages in an LDS ring filled by
+// buffer loads that write LDS directly (no registers, one 1 KB block per wave
+// instruction), so NS - 1 k-blocks of loads stay in flight while the waves
+// multiply; one barrier per k-block.
 //
-// Epilogues are the reference's (see fgm_decode.hip): int8 is exact int32
-// over all of K then (float)acc * (b_scale * a_scale); int4 drains its int32
-// accumulators into an fp32 fma chain at the end of every scale group, in
-// ascending group order, then multiplies by a_scale.
+// MFMA operand mapping (lane l, h = l >> 5, row / column l & 31): step s of
+// the k-block (two 32-wide steps) gives operand byte b = 4t + e of half h the
+// k = 32s + 16h + 4t + e, i.e. k-tile row r = 8s + 4h + t of the weight tile.
+// Output: lane l, register r holds row 8(r/4) + 4h + r%4, column l & 31.
+//
+// LDS layouts are permutations of the HBM bytes chosen so that every fragment
+// read is free of bank conflicts:
+//   A, per 16-row m-block (1 KB): row i at 64 i, its 16-byte chunk q at slot
+//     q ^ ((i >> 2) & 3); the fragment of step s, half h is chunk 2s + h of
+//     the row: one ds_read_b128.
+//   int8 B, per n-block (1 KB + 64 B pad): weight row r (4 k, 16 columns) at
+//     row position rho(r) = 8s + 4h + ((t + 2h) & 3); a fragment is four
+//     ds_read_b32 (rows 8s + 4h + t, column c).
+//   int4 B, per pair of n-blocks (1 KB): the second n-block's rows rotated by
+//     two; four ds_read_b32 per fragment, then the lane keeps its column's
+//     nibbles in the high half of each byte (x16, see fgm_decode.hip).
+//
+// Epilogues are the reference's: int8 is exact int32 over all of K, then
+// (float)acc * (b_scale * a_scale) (vnni_gemm.c:206-219); int4 drains its
+// int32 accumulators into an fp32 fma chain at the end of every scale group,
+// in ascending group order, then multiplies by a_scale (vnni_gemm.c:258-285,
+// 316-321).  The int4 sums are 16 * acc and the parked scales f32(s) / 16, an
+// exact product.
+#include <type_traits>
+
 #include "fgm_common.h"
 #include "fgm_kernels.h"
 
 namespace {
 
-constexpr int PITCH = 80;        // LDS bytes per row / column (64 + 16 pad)
-constexpr int BLK = 16 * PITCH;  // one 16x64 operand block in LDS
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 FGM_DEV GemmProb pick(const GemmBatch& bt) {
   const int b = blockIdx.x;
@@ -35,250 +50,396 @@ FGM_DEV GemmProb pick(const GemmBatch& bt) {
   return p;
 }
 
-template <int BITS, int BM, int BN, int D>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmBatch bt) {
-  constexpr int MBL = BM / 16, NBL = BN / 16;    // operand blocks per stage
-  constexpr int MS = BM / 32, NS = BN / 32;      // 16x16 subtiles per wave
-  constexpr int STAGE = (MBL + NBL) * BLK;
-  constexpr int ACH = BM * 4 / 256;              // 16-byte A chunks per thread
-  constexpr int BCH_TOT = (BITS == 8) ? BN * 4 : BN * 2;
-  constexpr int BCH = (BCH_TOT + 255) / 256;     // 16-byte B chunks per thread
-  static_assert(ACH >= 1 && MS >= 1 && NS >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+FGM_DEV v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
 
+// A raw buffer descriptor as four scalars (gfx9 layout: base, stride 0,
+// num_records, the same flags as make_rsrc).
+FGM_DEV v4i rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+             __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xFFFF)),
+             __builtin_amdgcn_readfirstlane((int)bytes), FGM_BUF_FLAGS};
+}
+
+// One 16-byte chunk per lane from buffer offset voff + soff to LDS byte
+// address lds + 16 * lane (buffer_load_dwordx4 ... lds).  Out-of-range lanes
+// read zeros.  The compiler does not see these loads: the caller waits for
+// them with wait_vm.
+FGM_DEV void dma16(v4i rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+  // lds and soff are wave-uniform: keep them in scalar registers
+  const int l0 = __builtin_amdgcn_readfirstlane((int)lds);
+  const int s0 = __builtin_amdgcn_readfirstlane((int)soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(l0), "v"(voff), "s"(rs), "s"(s0)
+               : "memory", "m0");
+}
+
+template <int N>
+FGM_DEV void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Row position of weight-tile row r in the int8 LDS layout (an involution).
+FGM_DEV int rho(int r) { return (r & ~3) | ((r + 2 * ((r >> 2) & 1)) & 3); }
+
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS>
+struct Cfg {
+  static constexpr int NW = WGM * WGN, T = 64 * NW;
+  static constexpr int BM = 32 * WMT * WGM, BN = 32 * WNT * WGN;
+  static constexpr int MBL = BM / 16, NBL = BN / 16;
+  static constexpr int BUNIT = BITS == 8 ? 1088 : 1024;     // LDS bytes per B unit
+  static constexpr int BUNITS = BITS == 8 ? NBL : NBL / 2;  // B units per stage
+  static constexpr int A_BYTES = MBL * 1024;
+  static constexpr int B_BYTES = BUNITS * BUNIT;
+  static constexpr int S_BYTES = BITS == 4 ? 1024 : 0;      // int4 group scales
+  static constexpr int KBLK = A_BYTES + B_BYTES + S_BYTES;  // one k-block
+  static constexpr int STAGE = KS * KBLK;                     // KS k-blocks per ring slot
+  // DMA instructions per wave per k-block (A units, B units, the int4
+  // scales) and per stage
+  static constexpr int UK = (MBL + NW - 1) / NW + (BUNITS + NW - 1) / NW + (BITS == 4 ? 1 : 0);
+  static constexpr int U = KS * UK;
+  static_assert((NS - 2) * U <= 63, "vmcnt range");
+  // the ring, a 1 KB sink for the zero loads that keep the per-wave load
+  // count fixed, the epilogue scales
+  static constexpr size_t TRASH = (size_t)NS * STAGE;
+  static constexpr size_t LDS = TRASH + 1024 + (BM + BN) * 4;
+  static_assert(BITS == 8 || NBL % 2 == 0, "int4 tiles come in n-block pairs");
+};
+
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
+  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick(bt);
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, g = l >> 4, j = l & 15;
-  const int wm = w & 1, wn = w >> 1;
+  const int tid = threadIdx.x, w = wave_id(), l = tid & 63, h = l >> 5, l32 = l & 31;
+  const int wm = w % WGM, wn = w / WGM;
 
   const int M = a.M, N = a.N, KB = a.K >> 6;
-  const int MT = (M + BM - 1) / BM;
-  const int NT = (a.nblocks + NBL - 1) / NBL;
-  int bid = blockIdx.x - a.wg0;
+  const int MT = (M + C::BM - 1) / C::BM;
+  const int NT = (a.nblocks + C::NBL - 1) / C::NBL;
   const int ntiles = MT * NT;
-  // XCD-aware order (workgroup ids go round-robin over the 8 XCDs): give each
-  // XCD a contiguous run of tiles, m fastest, so tiles sharing B share an L2.
+  int bid = blockIdx.x - a.wg0;
+  // Workgroup ids go round-robin over the 8 XCDs: give each XCD a contiguous
+  // run of tiles in grouped order (GM m-tiles at a time, n within a group),
+  // so that the tiles an L2 serves at once share A rows and B columns.
   if ((ntiles & 7) == 0 && (a.wg0 & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
-  const int mt = bid % MT, nt = bid / MT;
+  const int GM = MT < 4 ? MT : 4;
+  const int grp = bid / (GM * NT), inr = bid - grp * GM * NT;
+  const int gm = (MT - grp * GM) < GM ? (MT - grp * GM) : GM;  // m-tiles in this group
+  const int mtile = grp * GM + inr % gm, ntile = inr / gm;
   const int MBtot = (M + 15) >> 4;
-  const int mb0 = mt * MBL;
-  const int nb0 = a.n0 + nt * NBL;
+  const int mb0 = mtile * C::MBL;              // first m-block of the tile
+  const int nb0 = a.n0 + ntile * C::NBL;       // first n-block of the tile
   const int nbend = a.n0 + a.nblocks;
-  const int gk = (BITS == 4) ? (a.group >> 6) : 1;
-  const bool want_scales = BITS == 4 && a.acc_out == nullptr;
+  const int gk = BITS == 4 ? a.group >> 6 : 1;
 
-  v4i ra[D][ACH], rb[D][BCH];
-  float sreg[D][NS];
-
-  auto gload = [&](int kb, v4i* rA, v4i* rB, float* sc) {
+  // ---- DMA plan: wave w issues A units w, w + NW, ..., B units likewise,
+  // and wave 0 the int4 scale unit; slots past the unit count load zeros
+  // (FGM_OOB), so every wave issues exactly U loads per stage
+  constexpr int UA = (C::MBL + C::NW - 1) / C::NW, UB = (C::BUNITS + C::NW - 1) / C::NW;
+  constexpr int US = BITS == 4 ? 1 : 0;
+  static_assert(UA + UB + US == C::UK, "unit plan");
+  const v4i ra = rsrc_words(a.A, (uint32_t)MBtot * KB * 1024);
+  const v4i rb = rsrc_words(a.B, (uint32_t)nbend * KB * (BITS == 8 ? 1024 : 512));
+  // int4 group scales (raw-accumulator mode has none: an empty range, every
+  // lane out of range)
+  const v4i rsc = rsrc_words(a.b_scale, (BITS == 4 && !RAW) ? (uint32_t)(KB / gk) * N * 2 : 0);
+  uint32_t avoffs[UA], alds[UA], bvoffs[UB], blds[UB], svoff = FGM_OOB;
+  // LDS offsets are relative to a stage; a slot past the unit count targets
+  // the sink (TRASH - stage base is resolved in issue())
+  constexpr uint32_t SINK = 0xFFFFFFFFu;
 #pragma unroll
-    for (int u = 0; u < ACH; u++) {
-      const int c = tid + 256 * u;
-      const int mbl = c >> 6, i = (c & 63) >> 2, h = c & 3;
-      const int mb = mb0 + mbl;
-      rA[u] = v4i{0, 0, 0, 0};
-      if (mb < MBtot) rA[u] = *(const v4i*)(a.A + (((size_t)mb * KB + kb) * 16 + i) * 64 + 16 * h);
-    }
+  for (int i = 0; i < UA; i++) {
+    const int u = w + C::NW * i, mb = mb0 + u, row = l >> 2, q = (l & 3) ^ ((row >> 2) & 3);
+    alds[i] = u < C::MBL ? u * 1024 : SINK;
+    avoffs[i] = (u < C::MBL && mb < MBtot) ? (uint32_t)mb * KB * 1024 + row * 64 + 16 * q : FGM_OOB;
+  }
 #pragma unroll
-    for (int u = 0; u < BCH; u++) {
-      const int c = tid + 256 * u;
-      rB[u] = v4i{0, 0, 0, 0};
-      if (c < BCH_TOT) {
-        if (BITS == 8) {
-          const int nbl = c >> 6, r = (c & 63) >> 2, h = c & 3, nb = nb0 + nbl;
-          if (nb < nbend)
-            rB[u] = __builtin_nontemporal_load((const v4i*)((const int8_t*)a.B +
-                                               ((size_t)nb * KB + kb) * 1024 + r * 64 + 16 * h));
-        } else {
-          const int nbl = c >> 5, r = (c & 31) >> 1, h = c & 1, nb = nb0 + nbl;
-          if (nb < nbend)
-            rB[u] = __builtin_nontemporal_load((const v4i*)((const uint8_t*)a.B +
-                                               ((size_t)nb * KB + kb) * 512 + r * 32 + 16 * h));
-        }
-      }
+  for (int i = 0; i < UB; i++) {
+    const int u = w + C::NW * i;
+    blds[i] = u < C::BUNITS ? C::A_BYTES + u * C::BUNIT : SINK;
+    bvoffs[i] = FGM_OOB;
+    if (BITS == 8) {
+      const int nb = nb0 + u, R = l >> 2, q = l & 3;
+      if (u < C::BUNITS && nb < nbend) bvoffs[i] = (uint32_t)nb * KB * 1024 + rho(R) * 64 + 16 * q;
+    } else {
+      const int n2 = l >> 5, R = (l & 31) >> 1, q = l & 1;
+      const int nb = nb0 + 2 * u + n2, r = n2 ? ((R - 2) & 15) : R;
+      if (u < C::BUNITS && nb < nbend) bvoffs[i] = (uint32_t)nb * KB * 512 + r * 32 + 16 * q;
     }
-    if (want_scales) {
-      const uint16_t* bsp = (const uint16_t*)a.b_scale + (size_t)(kb / gk) * N;
+  }
+  if (BITS == 4 && !RAW && w == 0) {
+    const int col = nb0 * 16 + 8 * l;
+    if (l < C::BN / 8 && col < nbend * 16) svoff = (uint32_t)col * 2;
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+  const uint32_t sink = lds0 + (uint32_t)C::TRASH;
+  // loads of k-block j of stage sidx (k-blocks KS*sidx ...) into ring slot
+  // `slot`; zeros past K, which land in k-blocks that are never multiplied
+  auto issue_part = [&](int sidx, int slot, int j) {
+    const int kb = sidx * KS + j;
+    const bool live = kb < KB;
+    const uint32_t sb = lds0 + slot * C::STAGE + j * C::KBLK;
 #pragma unroll
-      for (int ns = 0; ns < NS; ns++) {
-        const int nb = nb0 + wn * NS + ns;
-        sc[ns] = nb < nbend ? f16_bits_to_f32(bsp[nb * 16 + j]) : 0.0f;
-      }
-    }
+    for (int i = 0; i < UA; i++)
+      dma16(ra, alds[i] == SINK ? sink : sb + alds[i], live ? avoffs[i] : FGM_OOB, (uint32_t)kb * 1024);
+#pragma unroll
+    for (int i = 0; i < UB; i++)
+      dma16(rb, blds[i] == SINK ? sink : sb + blds[i], live ? bvoffs[i] : FGM_OOB,
+            (uint32_t)kb * (BITS == 8 ? 1024 : 512));
+    if (BITS == 4)
+      dma16(rsc, w == 0 ? sb + C::A_BYTES + C::B_BYTES : sink, live ? svoff : FGM_OOB,
+            live ? (uint32_t)(kb / gk) * N * 2 : 0);
   };
-  auto swrite = [&](char* st, const v4i* rA, const v4i* rB) {
+  auto issue = [&](int sidx, int slot) {
 #pragma unroll
-    for (int u = 0; u < ACH; u++) {
-      const int c = tid + 256 * u;
-      const int mbl = c >> 6, i = (c & 63) >> 2, h = c & 3;
-      *(v4i*)(st + mbl * BLK + i * PITCH + 16 * h) = rA[u];
+    for (int j = 0; j < KS; j++) issue_part(sidx, slot, j);
+  };
+
+  // epilogue scales in LDS, after the ring: a_scale [BM], (int8) b_scale [BN]
+  float* ASC = (float*)(smem + C::TRASH + 1024);
+  float* BSC = ASC + C::BM;
+  if (!RAW) {
+    for (int i = tid; i < C::BM; i += C::T) {
+      const int m = mtile * C::BM + i;
+      ASC[i] = m < M ? a.a_scale[m] : 0.0f;
     }
-    char* bs = st + MBL * BLK;
+    if (BITS == 8)
+      for (int i = tid; i < C::BN; i += C::T) {
+        const int n = nb0 * 16 + i;
+        BSC[i] = n < nbend * 16 ? ((const float*)a.b_scale)[n] : 0.0f;
+      }
+  }
+
+  // ---- prologue: NS - 1 stages in flight
 #pragma unroll
-    for (int u = 0; u < BCH; u++) {
-      const int c = tid + 256 * u;
-      if (c < BCH_TOT) {
-        if (BITS == 8) {
-          const int nbl = c >> 6, r = (c & 63) >> 2, h = c & 3;
-          char* base = bs + nbl * BLK + 4 * r;
+  for (int s = 0; s < NS - 1; s++) issue(s, s);
+  wait_vm<(NS - 2) * C::U>();
+  __syncthreads();  // stage 0 in LDS
+  issue(NS - 1, NS - 1);
+
+  v16i acc[WMT][WNT];
+  float cf[BITS == 4 ? WMT : 1][BITS == 4 ? WNT : 1][16];
 #pragma unroll
-          for (int e = 0; e < 4; e++) *(int32_t*)(base + (4 * h + e) * PITCH) = rB[u][e];
-        } else {
-          const int nbl = c >> 5, r = (c & 31) >> 1, h = c & 1;
-          char* base = bs + nbl * BLK + 4 * r;
+  for (int x = 0; x < WMT; x++)
 #pragma unroll
-          for (int d = 0; d < 4; d++) {
-            const uint32_t v = (uint32_t)rB[u][d];
-            *(uint32_t*)(base + (4 * h + d) * PITCH) = nib4_to_i8x4(v & 0x0F0F0F0Fu);
-            *(uint32_t*)(base + (8 + 4 * h + d) * PITCH) = nib4_to_i8x4((v >> 4) & 0x0F0F0F0Fu);
+    for (int y = 0; y < WNT; y++) {
+      acc[x][y] = v16i{};
+      if (BITS == 4)
+#pragma unroll
+        for (int r = 0; r < 16; r++) cf[x][y][r] = 0.0f;
+    }
+
+  // per-lane fragment addresses within a stage
+  uint32_t aoff[WMT][2];  // [m tile][step]: ds_read_b128
+#pragma unroll
+  for (int x = 0; x < WMT; x++) {
+    const int row = wm * WMT * 32 + x * 32 + l32, mbl = row >> 4, i = row & 15;
+#pragma unroll
+    for (int s = 0; s < 2; s++) aoff[x][s] = mbl * 1024 + i * 64 + 16 * ((2 * s + h) ^ ((i >> 2) & 3));
+  }
+  uint32_t boff[WNT];     // + row offset below
+  int bsh = 0;            // int4: nibble shift of this lane's column
+#pragma unroll
+  for (int y = 0; y < WNT; y++) {
+    const int col = wn * WNT * 32 + y * 32 + l32, nbl = col >> 4, c = col & 15;
+    if (BITS == 8) {
+      boff[y] = C::A_BYTES + nbl * C::BUNIT + 4 * c;
+    } else {
+      boff[y] = C::A_BYTES + (nbl >> 1) * 1024 + (nbl & 1) * 512 + 4 * (c & 7);
+      bsh = c < 8 ? 4 : 0;
+    }
+  }
+  // int4: this lane's column of the staged scales, per n tile
+  uint32_t soffl[WNT];
+#pragma unroll
+  for (int y = 0; y < WNT; y++) soffl[y] = C::A_BYTES + C::B_BYTES + 2 * (wn * WNT * 32 + y * 32 + l32);
+
+  // Fragments of one k-block: both 32-wide steps; int4 also its scales.
+  v4i af[2][2][WMT], bf[2][2][WNT];
+  float scl[2][WNT];
+  auto fetch = [&](auto bufc, const char* st) {
+    constexpr int buf = decltype(bufc)::value;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+      for (int x = 0; x < WMT; x++) af[buf][s][x] = *(const v4i*)(st + aoff[x][s]);
+#pragma unroll
+      for (int y = 0; y < WNT; y++) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int r = 8 * s + 4 * h + t;
+          if (BITS == 8) {
+            bf[buf][s][y][t] = *(const int32_t*)(st + boff[y] + rho(r) * 64);
+          } else {
+            const int nbl = ((wn * WNT * 32 + y * 32 + l32) >> 4) & 1;
+            const uint32_t x = *(const uint32_t*)(st + boff[y] + ((r + 2 * nbl) & 15) * 32);
+            bf[buf][s][y][t] = (int)((x << bsh) & 0xF0F0F0F0u);
           }
         }
       }
     }
+    if (BITS == 4 && !RAW)
+#pragma unroll
+      for (int y = 0; y < WNT; y++) scl[buf][y] = f16_bits_to_f32(*(const uint16_t*)(st + soffl[y])) * 0.0625f;
   };
 
-  v4i acc[MS][NS];
-  float cf[MS][NS][4];
+  // Software pipeline: the multiplies of k-block kb are issued first; while
+  // the matrix cores work, the wave waits for k-block kb + 1, refills the
+  // slot of kb and reads kb + 1's fragments into the other register set.
+  // The register set of k-block kb is kb & 1 (the loop runs two k-blocks per
+  // trip, so the set index is a constant).  Within a stage the next k-block's
+  // fragments are read while this one multiplies; at the end of a stage the
+  // wave waits for the next stage, refills the slot of this one and reads
+  // the next stage's first k-block.
+  const int KBR = (KB + KS - 1) / KS * KS;
+  auto step = [&](int kb, auto setc) {
+    constexpr int cur = decltype(setc)::value;
+    const bool fresh = BITS == 4 && (kb % gk) == 0;
+    if (kb < KB) {
 #pragma unroll
-  for (int x = 0; x < MS; x++)
+      for (int s = 0; s < 2; s++)
 #pragma unroll
-    for (int y = 0; y < NS; y++) {
-      acc[x][y] = v4i{0, 0, 0, 0};
+        for (int x = 0; x < WMT; x++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) cf[x][y][r] = 0.0f;
+          for (int y = 0; y < WNT; y++)
+            acc[x][y] = (fresh && s == 0) ? mfma32(af[cur][s][x], bf[cur][s][y], v16i{})
+                                          : mfma32(af[cur][s][x], bf[cur][s][y], acc[x][y]);
     }
-
-  // prologue: D stages in flight, stage 0 in LDS
-#pragma unroll
-  for (int s = 0; s < D; s++)
-    if (s < KB) gload(s, ra[s], rb[s], sreg[s]);
-  swrite(smem, ra[0], rb[0]);
-  float scur[NS];  // int4: the scales of the stage being multiplied
-#pragma unroll
-  for (int ns = 0; ns < NS; ns++) scur[ns] = sreg[0][ns];
-  // slot s % D holds stage s: slot 0 moves on to stage D
-  if (D < KB) gload(D, ra[0], rb[0], sreg[0]);
-  __syncthreads();
-
-  for (int kb0 = 0; kb0 < KB; kb0 += D) {
-#pragma unroll
-    for (int u = 0; u < D; u++) {
-      const int kb = kb0 + u;
-      if (kb < KB) {
-        // ring slot of stage kb + 1: move it to LDS, keep its scales, then
-        // refill the slot with stage kb + 1 + D
-        const int nx = (u + 1) % D;
-        float snext[NS];
-#pragma unroll
-        for (int ns = 0; ns < NS; ns++) snext[ns] = sreg[nx][ns];
-        if (kb + 1 < KB) swrite(smem + ((kb + 1) & 1) * STAGE, ra[nx], rb[nx]);
-        if (kb + 1 + D < KB) gload(kb + 1 + D, ra[nx], rb[nx], sreg[nx]);
-
-        const char* st = smem + (kb & 1) * STAGE;
-        v4i af[MS], bf[NS];
-#pragma unroll
-        for (int ms = 0; ms < MS; ms++)
-          af[ms] = *(const v4i*)(st + (wm * MS + ms) * BLK + j * PITCH + 16 * g);
-#pragma unroll
-        for (int ns = 0; ns < NS; ns++)
-          bf[ns] = *(const v4i*)(st + (MBL + wn * NS + ns) * BLK + j * PITCH + 16 * g);
-#pragma unroll
-        for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-          for (int ns = 0; ns < NS; ns++) acc[ms][ns] = mfma16(af[ms], bf[ns], acc[ms][ns]);
-
-        if (BITS == 4 && ((kb + 1) % gk) == 0) {
-          const int gi = kb / gk;
-#pragma unroll
-          for (int ms = 0; ms < MS; ms++)
-#pragma unroll
-            for (int ns = 0; ns < NS; ns++) {
-              if (a.acc_out) {
-                const int nb = nb0 + wn * NS + ns;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                  const int m = (mb0 + wm * MS + ms) * 16 + 4 * g + r;
-                  if (m < M && nb < nbend)
-                    a.acc_out[((size_t)gi * M + m) * a.ldacc + nb * 16 + j] = acc[ms][ns][r];
-                }
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                  cf[ms][ns][r] = __builtin_fmaf((float)acc[ms][ns][r], scur[ns], cf[ms][ns][r]);
-              }
-              acc[ms][ns] = v4i{0, 0, 0, 0};
-            }
-        }
-#pragma unroll
-        for (int ns = 0; ns < NS; ns++) scur[ns] = snext[ns];
-        __syncthreads();
+    // The refill of a slot is spread over the next stage: k-block 0 of stage
+    // sidx + NS right after the barrier that frees slot sidx, k-block j + 1
+    // after the multiplies of k-block j of stage sidx + 1.
+    if (kb + 1 < KBR) {
+      const int sidx = kb / KS, j = kb - sidx * KS;
+      if (j + 1 < KS) {
+        if (sidx >= 1) issue_part(sidx - 1 + NS, (sidx - 1) % NS, j + 1);
+        fetch(std::integral_constant<int, cur ^ 1>{}, smem + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
+      } else {
+        wait_vm<(NS - 2) * C::U>();
+        __syncthreads();  // stage sidx + 1 in LDS; every wave is done with sidx's slot
+        issue_part(sidx + NS, sidx % NS, 0);
+        fetch(std::integral_constant<int, cur ^ 1>{}, smem + ((sidx + 1) % NS) * C::STAGE);
       }
     }
+    if (BITS == 4 && kb < KB && ((kb + 1) % gk) == 0) {
+      const int gi = kb / gk;
+#pragma unroll
+      for (int y = 0; y < WNT; y++) {
+        const int n = nb0 * 16 + wn * WNT * 32 + y * 32 + l32;
+        if (RAW) {
+#pragma unroll
+          for (int x = 0; x < WMT; x++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const int m = mtile * C::BM + wm * WMT * 32 + x * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (m < M && n < nbend * 16) a.acc_out[((size_t)gi * M + m) * a.ldacc + n] = acc[x][y][r] >> 4;
+            }
+        } else {
+          const float sc = scl[cur][y];
+#pragma unroll
+          for (int x = 0; x < WMT; x++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) cf[x][y][r] = __builtin_fmaf((float)acc[x][y][r], sc, cf[x][y][r]);
+        }
+      }
+    }
+  };
+  fetch(std::integral_constant<int, 0>{}, smem);
+  for (int kb = 0; kb < KBR; kb += 2) {
+    step(kb, std::integral_constant<int, 0>{});
+    if (kb + 1 < KBR) step(kb + 1, std::integral_constant<int, 1>{});
   }
+  wait_vm<0>();
 
   // ---- epilogue
+  if (BITS == 4 && RAW) return;
 #pragma unroll
-  for (int ns = 0; ns < NS; ns++) {
-    const int nb = nb0 + wn * NS + ns;
-    if (nb >= nbend) continue;
-    const int n = nb * 16 + j;
-    const float bsn = (BITS == 8 && !a.acc_out) ? ((const float*)a.b_scale)[n] : 0.0f;
+  for (int y = 0; y < WNT; y++) {
+    const int coll = wn * WNT * 32 + y * 32 + l32, n = nb0 * 16 + coll;
+    if (n >= nbend * 16) continue;
+    const float bsn = (BITS == 8 && !RAW) ? BSC[coll] : 0.0f;
 #pragma unroll
-    for (int ms = 0; ms < MS; ms++)
+    for (int x = 0; x < WMT; x++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = (mb0 + wm * MS + ms) * 16 + 4 * g + r;
+      for (int r = 0; r < 16; r++) {
+        const int rowl = wm * WMT * 32 + x * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int m = mtile * C::BM + rowl;
         if (m >= M) continue;
         if (BITS == 8) {
-          if (a.acc_out) a.acc_out[(size_t)m * a.ldacc + n] = acc[ms][ns][r];
-          else a.C[(size_t)m * a.ldc + n] = (float)acc[ms][ns][r] * (bsn * a.a_scale[m]);
-        } else if (!a.acc_out) {
-          a.C[(size_t)m * a.ldc + n] = cf[ms][ns][r] * a.a_scale[m];
+          if (RAW) a.acc_out[(size_t)m * a.ldacc + n] = acc[x][y][r];
+          else a.C[(size_t)m * a.ldc + n] = (float)acc[x][y][r] * (bsn * ASC[rowl]);
+        } else {
+          a.C[(size_t)m * a.ldc + n] = cf[x][y][r] * ASC[rowl];
         }
       }
   }
 }
 
-template <int BITS, int BM, int BN, int D>
-hipError_t launch(const GemmBatch& in, hipStream_t st) {
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW>
+hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
+  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
+  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, RAW>;
+  static hipError_t attr =
+      hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
+  if (attr != hipSuccess) return attr;
   GemmBatch b = in;
   int nwg = 0;
   for (int i = 0; i < b.count; i++) {
     GemmProb& p = b.p[i];
     p.wg0 = nwg;
-    nwg += ((p.M + BM - 1) / BM) * ((p.nblocks + BN / 16 - 1) / (BN / 16));
+    nwg += ((p.M + C::BM - 1) / C::BM) * ((p.nblocks + C::NBL - 1) / C::NBL);
   }
   if (nwg == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<BITS, BM, BN, D>), dim3(nwg), dim3(256), 0, st, b);
+  hipLaunchKernelGGL(k, dim3(nwg), dim3(C::T), C::LDS, st, b);
   return hipGetLastError();
 }
 
-// Tile shape: the largest tile that still gives about one tile per CU.
-int pick_tile(int bits, const GemmBatch& b) {
-  long t128 = 0, t256 = 0, t64 = 0;
-  int mmax = 0;
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS>
+hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
+  return b.p[0].acc_out ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, true>(b, st)
+                        : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false>(b, st);
+}
+
+// Tile shape and ring.  The kernel is bound by LDS reads unless two
+// workgroups share a CU (each hides the other's LDS latency), so the rings
+// are kept under 80 KB and the largest tile that still gives about two
+// workgroups per CU wins: 256 x 128, else 128 x 128, else 128 x 64.
+int pick_tile(const GemmBatch& b) {
+  long t256 = 0, t128 = 0;
   for (int i = 0; i < b.count; i++) {
     const GemmProb& p = b.p[i];
     t256 += (long)((p.M + 255) / 256) * ((p.nblocks + 7) / 8);
     t128 += (long)((p.M + 127) / 128) * ((p.nblocks + 7) / 8);
-    t64 += (long)((p.M + 127) / 128) * ((p.nblocks + 3) / 4);
-    if (p.M > mmax) mmax = p.M;
   }
-  if (bits == 8 && mmax > 128 && t256 >= 256) return 2;  // 256 x 128
-  if (t128 >= 192) return 1;                            // 128 x 128
-  (void)t64;
-  return 0;                                             // 128 x 64
+  if (t256 >= 480) return 2;
+  if (t128 >= 480) return 1;
+  return 0;
 }
 
 }  // namespace
 
-hipError_t fgm_launch_gemm(int bits, const GemmBatch& b, hipStream_t st) {
-  const int t = pick_tile(bits, b);
+hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
+  // one kernel variant per launch: raw-accumulator and scaled problems apart
+  for (int i = 1; i < in.count; i++)
+    if ((in.p[i].acc_out != nullptr) != (in.p[0].acc_out != nullptr)) {
+      GemmBatch x{}, y{};
+      for (int k = 0; k < in.count; k++) {
+        GemmBatch& d = (in.p[k].acc_out != nullptr) == (in.p[0].acc_out != nullptr) ? x : y;
+        d.p[d.count++] = in.p[k];
+      }
+      hipError_t e = fgm_launch_gemm(bits, x, st);
+      return e != hipSuccess ? e : fgm_launch_gemm(bits, y, st);
+    }
+  // ring: NS slots of KS k-blocks each, under 80 KB of LDS
+  const int t = pick_tile(in);
   if (bits == 8) {
-    if (t == 2) return launch<8, 256, 128, 4>(b, st);
-    if (t == 1) return launch<8, 128, 128, 4>(b, st);
-    return launch<8, 128, 64, 4>(b, st);
+    if (t == 2) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
+    if (t == 1) return launch_any<8, 2, 2, 2, 2, 2, 2>(in, st);
+    return launch_any<8, 2, 1, 2, 2, 2, 2>(in, st);
   }
-  if (t >= 1) return launch<4, 128, 128, 4>(b, st);
-  return launch<4, 128, 64, 4>(b, st);
+  if (t >= 1) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
+  return launch_any<4, 2, 1, 2, 2, 3, 1>(in, st);
 }
