@@ -16,10 +16,11 @@ plumbing) so host launch overhead stays off the GPU timeline.
 weights + f16 scales + packed A + a_scale + f32 C of both GEMMs plus the
 prep's fp32 read and packed-A write.
 
-`roofline` is for the dominant kernel (the int4 skinny GEMM, up shape): the
-average duration of one launch, measured with HIP events around a graph of
-48 back-to-back launches on the launch stream; `traffic` comes from the
-committed rocprofv3 PMC summary when present.
+`roofline` is for the dominant kernel, the step's GEMM launch (the int4
+skinny GEMM serving up and down in one launch): the average duration of one
+launch, measured with HIP events around a graph of 48 back-to-back launches
+on the launch stream; `traffic` comes from the committed rocprofv3 PMC
+summary (profiles/decode_q4g_m8_pair_traffic.txt).
 
 `cpu_baseline` runs the reference's own VNNI kernels (oracle/_ref, compiled
 from the reference sources) on this host's cores with the reference's thread
@@ -217,6 +218,22 @@ def extra_cfg1(gpu):
             "GB_s": b / dt / 1e9, "frac_hbm": b / dt / HBM_PEAK, "bytes_per_launch": b}
 
 
+def extra_int4_stream(gpu):
+    """The int4 skinny kernel's sustained rate on one large weight (M=8,
+    N=131072, K=2048, 134 MB; two copies > MALL): what the kernel streams
+    once the fixed per-launch cost (~2-3 us) is amortised.  Not a BASELINE
+    config; it bounds what a fused forward pass could reach."""
+    N, K = 131072, 2048
+    ws = [gpu.w4(N, K) for _ in range(2)]
+    x, qs, pa = gpu.act(8, K)
+    gpu.prep(x, qs, pa, 8, K)
+    c = gpu.t.empty(8, N, device=gpu.dev)
+    dt = kernel_avg(gpu, lambda i: gpu.q4g(8, N, K, pa, qs, ws[i % 2][0], ws[i % 2][1], c), 8, 3)
+    b = gemm_bytes(4, 8, N, K)
+    return {"workload": "int4 g64 M=8 N=131072 K=2048 (134 MB weights), one launch",
+            "us_per_launch": dt * 1e6, "GB_s": b / dt / 1e9, "frac_hbm": b / dt / HBM_PEAK}
+
+
 LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048),
          ("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
 
@@ -237,10 +254,32 @@ def extra_cfg3(gpu):
         tot_ops += ops
         tot_t += dt
         del ws
+    # the layer as the forward pass issues it: q/k/v on one activation in one
+    # launch, o, gate/up in one launch, down (forward.rs:484-641)
+    lw = [{name: gpu.w8(N, K) for name, N, K in LAYER} for _ in range(3)]
+    outs = {name: gpu.t.empty(256, N, device=gpu.dev) for name, N, K in LAYER}
+
+    def item(i, name):
+        N, K = next((N, K) for nm, N, K in LAYER if nm == name)
+        x, qs, pa = xs[K]
+        w = lw[i % 3][name]
+        return (8, 256, N, K, pa, qs, w[0], w[1], outs[name])
+
+    def layer(i):
+        gpu.gemm_many([item(i, "q"), item(i, "k"), item(i, "v")])
+        gpu.gemm_many([item(i, "o")])
+        gpu.gemm_many([item(i, "gate"), item(i, "up")])
+        gpu.gemm_many([item(i, "down")])
+    gs = gpu.graphs(layer, 12, 12)
+    gpu.time_graphs(gs, 2)
+    lt = gpu.time_graphs(gs, 5) / (5 * 12)
     return {"workload": "int8 prefill M=256, 7 projection shapes of one layer",
             "per_shape": res, "layer_us": tot_t * 1e6, "TOPS": tot_ops / tot_t / 1e12,
             "frac_mfma": tot_ops / tot_t / I8_PEAK,
-            "tokens_per_s_30_layers": 256 / (30 * tot_t)}
+            "layer_batched": {"launches": 4, "us": lt * 1e6, "TOPS": tot_ops / lt / 1e12,
+                              "frac_mfma": tot_ops / lt / I8_PEAK,
+                              "note": "q/k/v and gate/up each share one launch"},
+            "tokens_per_s_30_layers": 256 / (30 * lt)}
 
 
 def extra_cfg4(gpu):
@@ -384,8 +423,8 @@ def cpu_baseline(host, budget_s=10.0):
 # ------------------------------------------------------------------ main
 def read_traffic():
     """HBM bytes per launch of the dominant kernel from the committed PMC
-    summary (profiles/decode_q4g_m8_up_traffic.txt), or None."""
-    p = os.path.join(ROOT, "profiles", "decode_q4g_m8_up_traffic.txt")
+    summary (profiles/decode_q4g_m8_pair_traffic.txt), or None."""
+    p = os.path.join(ROOT, "profiles", "decode_q4g_m8_pair_traffic.txt")
     try:
         for line in open(p):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -434,8 +473,8 @@ def main():
     pair_b = up_b + down_b
     roof = {"bound": "hbm", "achieved": pair_b / pair_s / 1e9, "peak": HBM_PEAK / 1e9,
             "unit": "GB/s", "frac": pair_b / pair_s / HBM_PEAK, "traffic": read_traffic(),
-            "kernel": "decode_kernel<4,1,8>: the step's GEMM launch (int4 skinny GEMM, "
-                      "up N=8192 K=2048 and down N=2048 K=8192 in one launch, M=8)",
+            "kernel": "decode_kernel (int4, M <= 8 variant): the step's GEMM launch, "
+                      "up N=8192 K=2048 and down N=2048 K=8192 in one launch, M=8",
             "algorithmic_bytes_per_launch": pair_b, "us_per_launch": pair_s * 1e6,
             "timing": "HIP events around a graph of 48 back-to-back launches / 48",
             "single_shape_launches": {
@@ -445,8 +484,8 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        for name, fn in (("cfg1", extra_cfg1), ("cfg3", extra_cfg3), ("cfg5", extra_cfg5),
-                         ("cfg4", extra_cfg4)):
+        for name, fn in (("cfg1", extra_cfg1), ("int4_stream", extra_int4_stream),
+                         ("cfg3", extra_cfg3), ("cfg5", extra_cfg5), ("cfg4", extra_cfg4)):
             log("extra", name)
             try:
                 extra[name] = fn(gpu)
