@@ -77,9 +77,29 @@ FGM_DEV void dma16(v4i rs, uint32_t lds, uint32_t voff, uint32_t soff) {
                : "memory", "m0");
 }
 
+// One dword per lane to LDS byte address lds + 4 * lane (buffer_load_dword ...
+// lds); like dma16, waited for with wait_vm.
+FGM_DEV void dma4(v4i rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+  const int l0 = __builtin_amdgcn_readfirstlane((int)lds);
+  const int s0 = __builtin_amdgcn_readfirstlane((int)soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(l0), "v"(voff), "s"(rs), "s"(s0)
+               : "memory", "m0");
+}
+
 template <int N>
 FGM_DEV void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Compile-time loop: f(integral_constant<I>) for I = B .. E - 1.
+template <int B, int E, class F>
+FGM_DEV void sfor(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    sfor<B + 1, E>(f);
+  }
 }
 
 // Row position of weight-tile row r in the int8 LDS layout (an involution).
@@ -105,11 +125,11 @@ struct Cfg {
   // the ring, a 1 KB sink for the zero loads that keep the per-wave load
   // count fixed, the epilogue scales
   static constexpr size_t TRASH = (size_t)NS * STAGE;
-  static constexpr size_t LDS = TRASH + 1024 + (BM + BN) * 4;
+  static constexpr size_t LDS = TRASH + 1024 + (BM + (BN + 63) / 64 * 64) * 4;
   static_assert(BITS == 8 || NBL % 2 == 0, "int4 tiles come in n-block pairs");
 };
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW, bool G1>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -199,27 +219,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
     for (int j = 0; j < KS; j++) issue_part(sidx, slot, j);
   };
 
-  // epilogue scales in LDS, after the ring: a_scale [BM], (int8) b_scale [BN]
+  // epilogue scales in LDS, after the ring: a_scale [BM], (int8) b_scale [BN],
+  // brought in by 256-byte DMA chunks issued before the first stage, so that
+  // the wait for stage 0 covers them; rows past M and columns past n1 read
+  // zeros
   float* ASC = (float*)(smem + C::TRASH + 1024);
   float* BSC = ASC + C::BM;
-  if (!RAW) {
-    for (int i = tid; i < C::BM; i += C::T) {
-      const int m = mtile * C::BM + i;
-      ASC[i] = m < M ? a.a_scale[m] : 0.0f;
-    }
-    if (BITS == 8)
-      for (int i = tid; i < C::BN; i += C::T) {
-        const int n = nb0 * 16 + i;
-        BSC[i] = n < nbend * 16 ? ((const float*)a.b_scale)[n] : 0.0f;
-      }
-  }
-
-  // ---- prologue: NS - 1 stages in flight
+  {
+    constexpr int NCA = RAW ? 0 : C::BM / 64;
+    constexpr int NCB = (RAW || BITS == 4) ? 0 : (C::BN + 63) / 64;
+    constexpr int CH = (NCA + NCB + C::NW - 1) / C::NW;
+    const v4i rsa = rsrc_words(a.a_scale, RAW ? 0u : (uint32_t)M * 4);
+    const v4i rsb = rsrc_words(a.b_scale, NCB ? (uint32_t)nbend * 64 : 0u);
 #pragma unroll
-  for (int s = 0; s < NS - 1; s++) issue(s, s);
-  wait_vm<(NS - 2) * C::U>();
-  __syncthreads();  // stage 0 in LDS
-  issue(NS - 1, NS - 1);
+    for (int i = 0; i < CH; i++) {
+      const int c = w + C::NW * i;
+      if (c < NCA)
+        dma4(rsa, lds0 + (uint32_t)C::TRASH + 1024 + c * 256, (uint32_t)(mtile * C::BM + 64 * c + l) * 4, 0);
+      else if (c < NCA + NCB)
+        dma4(rsb, lds0 + (uint32_t)C::TRASH + 1024 + C::BM * 4 + (c - NCA) * 256,
+             (uint32_t)(nb0 * 16 + 64 * (c - NCA) + l) * 4, 0);
+      else
+        dma4(rsa, sink, FGM_OOB, 0);
+    }
+  }
 
   v16i acc[WMT][WNT];
   float cf[BITS == 4 ? WMT : 1][BITS == 4 ? WNT : 1][16];
@@ -258,104 +281,132 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
 #pragma unroll
   for (int y = 0; y < WNT; y++) soffl[y] = C::A_BYTES + C::B_BYTES + 2 * (wn * WNT * 32 + y * 32 + l32);
 
-  // Fragments of one k-block: both 32-wide steps; int4 also its scales.
+  // Fragments of one k-block in NG groups: group g is step s = g / (WMT + WNT)
+  // and then an A fragment (m tile r < WMT) or a B fragment (n tile r - WMT);
+  // the int4 group scale rides with the last B group.
+  constexpr int NG = 2 * (WMT + WNT), NM = 2 * WMT * WNT;
   v4i af[2][2][WMT], bf[2][2][WNT];
   float scl[2][WNT];
-  auto fetch = [&](auto bufc, const char* st) {
-    constexpr int buf = decltype(bufc)::value;
+  auto fetch_grp = [&](auto bufc, auto gc, const char* st) {
+    constexpr int buf = decltype(bufc)::value, g = decltype(gc)::value;
+    constexpr int s = g / (WMT + WNT), r = g % (WMT + WNT);
+    if constexpr (r < WMT) {
+      af[buf][s][r] = *(const v4i*)(st + aoff[r][s]);
+    } else {
+      constexpr int y = r - WMT;
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-#pragma unroll
-      for (int x = 0; x < WMT; x++) af[buf][s][x] = *(const v4i*)(st + aoff[x][s]);
-#pragma unroll
-      for (int y = 0; y < WNT; y++) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const int r = 8 * s + 4 * h + t;
-          if (BITS == 8) {
-            bf[buf][s][y][t] = *(const int32_t*)(st + boff[y] + rho(r) * 64);
-          } else {
-            const int nbl = ((wn * WNT * 32 + y * 32 + l32) >> 4) & 1;
-            const uint32_t x = *(const uint32_t*)(st + boff[y] + ((r + 2 * nbl) & 15) * 32);
-            bf[buf][s][y][t] = (int)((x << bsh) & 0xF0F0F0F0u);
-          }
+      for (int t = 0; t < 4; t++) {
+        const int rr = 8 * s + 4 * h + t;
+        if (BITS == 8) {
+          bf[buf][s][y][t] = *(const int32_t*)(st + boff[y] + rho(rr) * 64);
+        } else {
+          const int nbl = ((wn * WNT * 32 + y * 32 + l32) >> 4) & 1;
+          const uint32_t xv = *(const uint32_t*)(st + boff[y] + ((rr + 2 * nbl) & 15) * 32);
+          bf[buf][s][y][t] = (int)((xv << bsh) & 0xF0F0F0F0u);
         }
       }
+      if constexpr (BITS == 4 && !RAW && s == 1)
+        scl[buf][y] = f16_bits_to_f32(*(const uint16_t*)(st + soffl[y])) * 0.0625f;
     }
-    if (BITS == 4 && !RAW)
-#pragma unroll
-      for (int y = 0; y < WNT; y++) scl[buf][y] = f16_bits_to_f32(*(const uint16_t*)(st + soffl[y])) * 0.0625f;
   };
 
-  // Software pipeline: the multiplies of k-block kb are issued first; while
-  // the matrix cores work, the wave waits for k-block kb + 1, refills the
-  // slot of kb and reads kb + 1's fragments into the other register set.
-  // The register set of k-block kb is kb & 1 (the loop runs two k-blocks per
-  // trip, so the set index is a constant).  Within a stage the next k-block's
-  // fragments are read while this one multiplies; at the end of a stage the
-  // wave waits for the next stage, refills the slot of this one and reads
-  // the next stage's first k-block.
-  const int KBR = (KB + KS - 1) / KS * KS;
-  auto step = [&](int kb, auto setc) {
+  // The multiplies of one k-block (register set cur) with the next k-block's
+  // fragment reads and one DMA part of a refill placed between them, so that
+  // LDS latency and load issue hide behind the matrix cores.  An int4 group
+  // starts from a zero accumulator (every k-block when the group is 64).
+  auto mma = [&](auto setc, bool fresh, int rs, int rslot, int rj, const char* nst) {
     constexpr int cur = decltype(setc)::value;
-    const bool fresh = BITS == 4 && (kb % gk) == 0;
-    if (kb < KB) {
+    sfor<0, NM>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      constexpr int s = m / (WMT * WNT), x = (m / WNT) % WMT, y = m % WNT;
+      if constexpr (BITS == 4 && s == 0) {
+        if constexpr (G1) acc[x][y] = mfma32(af[cur][0][x], bf[cur][0][y], v16i{});
+        else acc[x][y] = mfma32(af[cur][0][x], bf[cur][0][y], fresh ? v16i{} : acc[x][y]);
+      } else {
+        acc[x][y] = mfma32(af[cur][s][x], bf[cur][s][y], acc[x][y]);
+      }
+      if constexpr (m == 0) issue_part(rs, rslot, rj);
+      sfor<m * NG / NM, (m + 1) * NG / NM>(
+          [&](auto gc) { fetch_grp(std::integral_constant<int, cur ^ 1>{}, gc, nst); });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  // int4: at the end of a scale group, fold the group's sums into the fp32
+  // chain (or dump them raw)
+  auto drain = [&](auto setc, int kb) {
+    constexpr int cur = decltype(setc)::value;
+    if (BITS != 4 || kb >= KB || ((kb + 1) % gk) != 0) return;
+    const int gi = kb / gk;
 #pragma unroll
-      for (int s = 0; s < 2; s++)
+    for (int y = 0; y < WNT; y++) {
+      const int n = nb0 * 16 + wn * WNT * 32 + y * 32 + l32;
+      if (RAW) {
 #pragma unroll
         for (int x = 0; x < WMT; x++)
 #pragma unroll
-          for (int y = 0; y < WNT; y++)
-            acc[x][y] = (fresh && s == 0) ? mfma32(af[cur][s][x], bf[cur][s][y], v16i{})
-                                          : mfma32(af[cur][s][x], bf[cur][s][y], acc[x][y]);
-    }
-    // The refill of a slot is spread over the next stage: k-block 0 of stage
-    // sidx + NS right after the barrier that frees slot sidx, k-block j + 1
-    // after the multiplies of k-block j of stage sidx + 1.
-    if (kb + 1 < KBR) {
-      const int sidx = kb / KS, j = kb - sidx * KS;
-      if (j + 1 < KS) {
-        if (sidx >= 1) issue_part(sidx - 1 + NS, (sidx - 1) % NS, j + 1);
-        fetch(std::integral_constant<int, cur ^ 1>{}, smem + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
+          for (int r = 0; r < 16; r++) {
+            const int m = mtile * C::BM + wm * WMT * 32 + x * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m < M && n < nbend * 16) a.acc_out[((size_t)gi * M + m) * a.ldacc + n] = acc[x][y][r] >> 4;
+          }
       } else {
-        wait_vm<(NS - 2) * C::U>();
-        __syncthreads();  // stage sidx + 1 in LDS; every wave is done with sidx's slot
-        issue_part(sidx + NS, sidx % NS, 0);
-        fetch(std::integral_constant<int, cur ^ 1>{}, smem + ((sidx + 1) % NS) * C::STAGE);
-      }
-    }
-    if (BITS == 4 && kb < KB && ((kb + 1) % gk) == 0) {
-      const int gi = kb / gk;
+        const float sc = scl[cur][y];
 #pragma unroll
-      for (int y = 0; y < WNT; y++) {
-        const int n = nb0 * 16 + wn * WNT * 32 + y * 32 + l32;
-        if (RAW) {
+        for (int x = 0; x < WMT; x++)
 #pragma unroll
-          for (int x = 0; x < WMT; x++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-              const int m = mtile * C::BM + wm * WMT * 32 + x * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (m < M && n < nbend * 16) a.acc_out[((size_t)gi * M + m) * a.ldacc + n] = acc[x][y][r] >> 4;
-            }
-        } else {
-          const float sc = scl[cur][y];
-#pragma unroll
-          for (int x = 0; x < WMT; x++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) cf[x][y][r] = __builtin_fmaf((float)acc[x][y][r], sc, cf[x][y][r]);
-        }
+          for (int r = 0; r < 16; r++) cf[x][y][r] = __builtin_fmaf((float)acc[x][y][r], sc, cf[x][y][r]);
       }
     }
   };
-  fetch(std::integral_constant<int, 0>{}, smem);
-  for (int kb = 0; kb < KBR; kb += 2) {
-    step(kb, std::integral_constant<int, 0>{});
-    if (kb + 1 < KBR) step(kb + 1, std::integral_constant<int, 1>{});
+
+  // ---- prologue: stages 0 .. NS - 2 in flight, stage 0 landed, part 0 of
+  // stage NS - 1 issued (its other parts go out during stage 0)
+#pragma unroll
+  for (int s = 0; s < NS - 1; s++) issue(s, s);
+  wait_vm<(NS - 2) * C::U>();
+  __syncthreads();
+  issue_part(NS - 1, NS - 1, 0);
+  sfor<0, NG>([&](auto gc) {  // in group order, as the loop reads them
+    fetch_grp(std::integral_constant<int, 0>{}, gc, smem);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  // ---- main loop.  Stage sidx, k-block j: while k-block j multiplies, part
+  // j + 1 of the refill of the previous stage's slot goes out and k-block
+  // j + 1 is read.  At the last k-block of a stage the wave first waits for
+  // stage sidx + 1 (all its parts were issued during stage sidx) and the
+  // barrier frees slot sidx, whose refill (stage sidx + NS) starts.  Trips of
+  // U2 stages keep the register set of every k-block a constant; k-blocks
+  // past K hold zeros.
+  constexpr int U2 = KS % 2 == 0 ? 1 : 2;
+  const int NSTG = (KB + KS * U2 - 1) / (KS * U2) * U2;
+  for (int sb = 0; sb < NSTG; sb += U2) {
+    sfor<0, U2 * KS>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, u = i / KS, j = i % KS, cur = i & 1;
+      const int sidx = sb + u, kb = sidx * KS + j;
+      const bool fresh = BITS == 4 && (kb % gk) == 0;
+      if constexpr (j + 1 < KS) {
+        mma(std::integral_constant<int, cur>{}, fresh, sidx - 1 + NS, (sidx + NS - 1) % NS, j + 1,
+            smem + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
+      } else {
+        wait_vm<(NS - 2) * C::U>();
+        __syncthreads();
+        mma(std::integral_constant<int, cur>{}, fresh, sidx + NS, sidx % NS, 0,
+            smem + ((sidx + 1) % NS) * C::STAGE);
+      }
+      drain(std::integral_constant<int, cur>{}, kb);
+    });
   }
   wait_vm<0>();
 
-  // ---- epilogue
+  // ---- epilogue: one buffer store per output; rows past M fall outside the
+  // tile's buffer range, columns past n1 are masked
   if (BITS == 4 && RAW) return;
+  const int mrow0 = mtile * C::BM;
+  const int mrows = M - mrow0 < C::BM ? M - mrow0 : C::BM;
+  const int ld = RAW ? a.ldacc : a.ldc;
+  const void* obase = RAW ? (const void*)(a.acc_out + (size_t)mrow0 * a.ldacc)
+                          : (const void*)(a.C + (size_t)mrow0 * a.ldc);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(obase, (uint32_t)mrows * (uint32_t)ld * 4u);
 #pragma unroll
   for (int y = 0; y < WNT; y++) {
     const int coll = wn * WNT * 32 + y * 32 + l32, n = nb0 * 16 + coll;
@@ -364,24 +415,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
 #pragma unroll
     for (int x = 0; x < WMT; x++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int rowl = wm * WMT * 32 + x * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int m = mtile * C::BM + rowl;
-        if (m >= M) continue;
-        if (BITS == 8) {
-          if (RAW) a.acc_out[(size_t)m * a.ldacc + n] = acc[x][y][r];
-          else a.C[(size_t)m * a.ldc + n] = (float)acc[x][y][r] * (bsn * ASC[rowl]);
-        } else {
-          a.C[(size_t)m * a.ldc + n] = cf[x][y][r] * ASC[rowl];
+      for (int q = 0; q < 4; q++) {
+        const int rowq = wm * WMT * 32 + x * 32 + 8 * q + 4 * h;  // rows rowq .. rowq + 3
+        const float4 as4 = RAW ? float4{} : *(const float4*)(ASC + rowq);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int r = 4 * q + e;
+          const float ase = e == 0 ? as4.x : e == 1 ? as4.y : e == 2 ? as4.z : as4.w;
+          uint32_t v;
+          if (BITS == 8 && RAW) v = (uint32_t)acc[x][y][r];
+          else if (BITS == 8) v = __float_as_uint((float)acc[x][y][r] * (bsn * ase));
+          else v = __float_as_uint(cf[x][y][r] * ase);
+          __builtin_amdgcn_raw_buffer_store_b32(v, ro, (int)(((uint32_t)(rowq + e) * (uint32_t)ld + (uint32_t)n) * 4u), 0, 0);
         }
       }
   }
 }
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW, bool G1>
 hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
-  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, RAW>;
+  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, RAW, G1>;
   static hipError_t attr =
       hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
   if (attr != hipSuccess) return attr;
@@ -389,6 +443,8 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
   int nwg = 0;
   for (int i = 0; i < b.count; i++) {
     GemmProb& p = b.p[i];
+    // the epilogue addresses one m-tile of C with 32-bit buffer offsets
+    if ((size_t)C::BM * (size_t)(p.acc_out ? p.ldacc : p.ldc) * 4 > 0xFFFFFFFFull) return hipErrorInvalidValue;
     p.wg0 = nwg;
     nwg += ((p.M + C::BM - 1) / C::BM) * ((p.nblocks + C::NBL - 1) / C::NBL);
   }
@@ -397,26 +453,22 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Variant: raw-accumulator dumps or scaled outputs; int4 with 64-wide groups
+// (a fresh accumulator every k-block) or the general group size.
 template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS>
 hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
-  return b.p[0].acc_out ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, true>(b, st)
-                        : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false>(b, st);
+  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, true, false>(b, st);
+  bool g1 = BITS == 4;
+  for (int i = 0; i < b.count; i++) g1 = g1 && b.p[i].group == 64;
+  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false, BITS == 4>(b, st)
+            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false, false>(b, st);
 }
 
-// Tile shape and ring.  The kernel is bound by LDS reads unless two
-// workgroups share a CU (each hides the other's LDS latency), so the rings
-// are kept under 80 KB and the largest tile that still gives about two
-// workgroups per CU wins: 256 x 128, else 128 x 128, else 128 x 64.
-int pick_tile(const GemmBatch& b) {
-  long t256 = 0, t128 = 0;
-  for (int i = 0; i < b.count; i++) {
-    const GemmProb& p = b.p[i];
-    t256 += (long)((p.M + 255) / 256) * ((p.nblocks + 7) / 8);
-    t128 += (long)((p.M + 127) / 128) * ((p.nblocks + 7) / 8);
-  }
-  if (t256 >= 480) return 2;
-  if (t128 >= 480) return 1;
-  return 0;
+// Workgroup tiles of a batch for a BM x BN tile.
+long tiles(const GemmBatch& b, int bm, int bn) {
+  long t = 0;
+  for (int i = 0; i < b.count; i++) t += (long)((b.p[i].M + bm - 1) / bm) * ((b.p[i].nblocks + bn / 16 - 1) / (bn / 16));
+  return t;
 }
 
 }  // namespace
@@ -433,13 +485,17 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
       hipError_t e = fgm_launch_gemm(bits, x, st);
       return e != hipSuccess ? e : fgm_launch_gemm(bits, y, st);
     }
-  // ring: NS slots of KS k-blocks each, under 80 KB of LDS
-  const int t = pick_tile(in);
+  // Tile and ring, from measured sweeps on MI355X: the largest tile that
+  // still puts a workgroup on (nearly) every CU; rings of NS slots of KS
+  // k-blocks.  Small problems (M = 256 projections) take 64 x 32 tiles with a
+  // deeper ring.
   if (bits == 8) {
-    if (t == 2) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
-    if (t == 1) return launch_any<8, 2, 2, 2, 2, 2, 2>(in, st);
-    return launch_any<8, 2, 1, 2, 2, 2, 2>(in, st);
+    if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
+    if (tiles(in, 128, 128) >= 240) return launch_any<8, 2, 2, 2, 2, 3, 2>(in, st);
+    if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 2, 2>(in, st);
+    return launch_any<8, 1, 1, 2, 1, 4, 2>(in, st);
   }
-  if (t >= 1) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
-  return launch_any<4, 2, 1, 2, 2, 3, 1>(in, st);
+  if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
+  if (tiles(in, 128, 64) >= 240) return launch_any<4, 2, 1, 2, 2, 2, 2>(in, st);
+  return launch_any<4, 1, 1, 2, 1, 4, 2>(in, st);
 }
