@@ -6,55 +6,73 @@
 // (the reference issues q/k/v and gate/up as separate GEMMs on one
 // activation, forward.rs:484,499-500,619-622).
 //
-// Work decomposition (chosen on the host, plan_split and fgm_launch_decode
-// below): a workgroup owns NBW 16-column n-blocks of one GEMM; each n-block's
-// K is split into KS contiguous ranges of TW 64-wide k-blocks (whole scale
-// groups for int4), one wave per range, so a workgroup has NBW * KS waves.
-// Every wave streams about 4 KB of weights with all of its loads in flight at
-// once: it issues the weight loads of up to CT tiles and their activation
-// fragments (L2-resident) before it multiplies anything.  Loop bounds and
-// tile indices are wave-uniform scalars; tiles past a wave's range and
-// activation rows >= M are masked by buffer range checks, not branches.
+// Work decomposition (plan_split / fgm_launch_decode below): a workgroup owns
+// NBW 16-column n-blocks of one GEMM and has NWS >= NBW * KS waves (those past
+// NBW * KS only take part in the barriers).  Each n-block's K is cut into 1 KB
+// units (two int4
+// k-tiles or one int8 k-tile) that its KS stream waves share round-robin:
+// unit u * KS + s belongs to wave s, so round u (one unit per wave) covers
+// TR = KS * (tiles per unit) consecutive k-tiles.
+//
+// Weight stream: each unit is one buffer_load_dwordx4 ... lds per wave (1 KB,
+// 16 contiguous bytes per lane, non-temporal) into a per-wave LDS ring of D
+// slots, up to D - 1 units in flight.  The lane loads a permuted 16-byte chunk
+// so that the fragment reads below are free of bank conflicts:
+//   int4 unit (two 512-byte tiles, 16-byte chunk c = 32 tile + 2 row + half):
+//     LDS chunk p holds HBM chunk p ^ (((p >> 3) & 3) << 1);
+//   int8 unit (one 1 KB tile, chunk c = 4 row + quarter):
+//     LDS chunk p holds HBM chunk p ^ (((p >> 4) & 3) << 2).
+// Activation fragments are plain 16-byte buffer loads (L2-resident), issued
+// with the unit they belong to: X vector-memory instructions per unit.  Units
+// are issued in order and never past a wave's last unit; the epilogue scales
+// (PRE loads) follow the first units.  So s_waitcnt vmcnt(X * units issued
+// after it + PRE if those came later) waits for exactly the unit that is
+// about to be multiplied.
 //
 // MFMA operand mapping (v_mfma_i32_16x16x64_i8, lane l = 16*g + j): A row j /
 // B column j, operand byte 4*t + e carries k = 16*g + 4*t + e, i.e. k-tile row
 // r = 4*g + t of the [k/4][n][k%4] layout.
-//   int8 B: the dword of row r, column j (byte 64*r + 4*j).
+//   int8 B: dword j of row r.
 //   int4 B: packed row r holds column c (c < 8) in the low and column c + 8
-//     in the high nibbles of its dword c (lanes j and j + 8 load the same
-//     dword).  The lane keeps its nibble in the high half of each byte:
-//     (x << 4) & 0xF0F0F0F0 for j < 8, x & 0xF0F0F0F0 for j >= 8.  A two's-
-//     complement nibble v in bits 7..4 of a byte is the int8 16 * v, so the
-//     MFMA accumulates exactly 16 * acc with two VALU operations per dword.
-//   A: one 16-byte load of the packed-A row per fragment.  M <= 8: lanes
-//     j < 8 load row j of an even k-tile and lanes j >= 8 row j - 8 of the
-//     following one; the odd tile's operand is moved into lanes 0-7 by a DPP
-//     rotation by 8 lanes.  Rows 8-15 of those products are never read.
+//     in the high nibbles of its dword c (lanes j and j + 8 read the same
+//     dword, an LDS broadcast).  The lane keeps its nibble in the high half of
+//     each byte: (x << 4) & 0xF0F0F0F0 for j < 8, x & 0xF0F0F0F0 for j >= 8.
+//     A two's-complement nibble v in bits 7..4 of a byte is the int8 16 * v,
+//     so the MFMA accumulates exactly 16 * acc.
+//   A: one 16-byte load of the packed-A row per fragment.  M <= 8 (HALF):
+//     lanes j < 8 load row j of the unit's first tile and lanes j >= 8 row
+//     j - 8 of its second; the second tile's operand is moved into lanes 0-7
+//     by a DPP rotation by 8 lanes.  Rows 8-15 of those products are unused.
 //     M > 8: one fragment per tile and 16-row m-block.
+//   Output: lane l, register r holds D[4*g + r][j].
 //
 // Epilogues, in the reference's operation order:
-//   q8c: the KS waves' int32 partials of an n-block are summed exactly in LDS,
+//   q8c: each stream wave accumulates int32 over its units; the KS partial
+//        sums of an n-block are added exactly in LDS, then
 //        C = (float)acc * (b_scale[n] * a_scale[m])          vnni_gemm.c:206-219
-//   q4g: each wave parks (float)(16 * acc_g) of its groups in LDS, laid out
-//        [m][column][group] with a padded group pitch so that the chain below
-//        reads four groups per 16-byte load without bank conflicts; the group
-//        scales are parked the same way, as f32(b_scale) / 16.  Both factors are powers of
-//        two, so (16 a) * (s / 16) is the exact product a * s and every fmaf
-//        rounds the same value as the reference's.  After one barrier one lane
-//        per output runs the chain in ascending g from 0:
-//        C = fmaf((float)acc_g, f16(b_scale[g][n]), C), then C *= a_scale[m]
-//                                                             vnni_gemm.c:258-285, 316-321
+//   q4g: the stream waves park every k-tile's sums (int32, 16 * acc) in LDS;
+//        after the stream one thread per output runs its chain in ascending
+//        k: the tile sums of a scale group are added exactly, and at the
+//        group's end
+//        C = fmaf((float)acc_g, f16(b_scale[g][n]), C)          vnni_gemm.c:258-285
+//        (the scale is kept as f32(b_scale) / 16: (16 a) * (s / 16) is the
+//        exact product a * s, so every fmaf rounds the reference's value);
+//        at the end C *= a_scale[m]                            vnni_gemm.c:316-321
 #include "fgm_common.h"
 #include "fgm_kernels.h"
 
 namespace {
 
 constexpr int MAX_WAVES = 16;
-constexpr int SPT = 4;             // group-scale dwords prefetched per thread
 constexpr int DPP_ROW_ROR8 = 0x128;
+constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thread
+#ifndef FGM_DEC_UPW
+#define FGM_DEC_UPW 4             // target units (1 KB) per stream wave
+#endif
+#ifndef FGM_DEC_NWMIN
+#define FGM_DEC_NWMIN 4           // smallest number of stream waves per workgroup
+#endif
 
-// The problem a workgroup belongs to, chosen with uniform selects so the
-// kernel-argument array is never indexed dynamically.
 FGM_DEV GemmProb pick(const GemmBatch& bt) {
   const int b = blockIdx.x;
   GemmProb p = bt.p[0];
@@ -64,363 +82,438 @@ FGM_DEV GemmProb pick(const GemmBatch& bt) {
   return p;
 }
 
+// Two 16-byte LDS reads by byte address, and waits for all but the last six
+// LDS operations (or for all of them) that also order the use of the given
+// registers after the wait.  LDS operations complete in issue order.
+template <int OFF>
+FGM_DEV void lds_read2x128(v4i& r0, v4i& r1, uint32_t a0, uint32_t a1) {
+  asm volatile("ds_read_b128 %0, %2 offset:%4\n\tds_read_b128 %1, %3 offset:%4"
+               : "=&v"(r0), "=&v"(r1)
+               : "v"(a0), "v"(a1), "n"(OFF)
+               : "memory");
+}
+FGM_DEV void lgkm_wait6(v4i& r0, v4i& r1) {
+  asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(r0), "+v"(r1) : : "memory");
+}
+FGM_DEV void lgkm_wait0(v4i& r0, v4i& r1) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1) : : "memory");
+}
+
 // the value of lane l ^ 8 (a rotation by 8 within every 16-lane row)
 FGM_DEV int ror8(int v) { return __builtin_amdgcn_mov_dpp(v, DPP_ROW_ROR8, 0xF, 0xF, false); }
 
-// Group pitch (words) of the parked int4 sums and scales: a multiple of four
-// with an odd number of quads, so that 16-byte reads of 16 consecutive
-// columns hit distinct banks.
-__host__ __device__ inline int group_pitch(int ng) {
-  const int r4 = (ng + 3) / 4 * 4;
+// Pitch (words) of a row of parked tile sums or group scales: a multiple of
+// four with an odd number of quads, so that 16-byte reads by consecutive rows
+// hit distinct banks.
+__host__ __device__ inline int pitch4(int n) {
+  const int r4 = (n + 3) / 4 * 4;
   return ((r4 / 4) & 1) ? r4 : r4 + 4;
 }
 
-template <int BITS, int MB, bool HALF, int CT, bool RAW>
-struct Stream {
-  static constexpr uint32_t TB = (BITS == 8) ? 1024u : 512u;  // bytes per k-tile
-  static constexpr int NA = HALF ? (CT + 1) / 2 : CT;         // A fragments per chunk
-  __amdgpu_buffer_rsrc_t rb, ra;
-  uint32_t bvoff;          // lane part of the weight-tile offset
-  uint32_t avoff[MB];      // lane part of the A-fragment offset (FGM_OOB if row >= M)
-  int h, sh;               // h = j >> 3; int4 nibble shift (4 for j < 8, else 0)
-  v4i acc[MB];
-  int32_t braw[CT][4];
-  v4i af[NA][MB];
-  int32_t* pb[MB][4];      // int4: group 0 of row 16 mb + 4 g + r, column j, in the
-                           // parked sums ([m][column][group]); null: not parked
-  int gk, gpos, gi;        // group length in k-blocks, position in it, group index
+// Ring slots per stream wave.
+#ifndef FGM_DEC_D
+#define FGM_DEC_D 5               // ring slots per stream wave (M <= 8)
+#endif
+__host__ __device__ constexpr int ring_depth(int bits, int MB, bool half) {
+  return half ? FGM_DEC_D : (bits == 8 ? 4 : (MB == 1 ? 4 : (MB == 2 ? 3 : 2)));
+}
 
-  // Loads of cnt (1..CT, wave-uniform) tiles starting at k-block t0, in the
-  // order the multiplies consume them (weights and activations of tile u
-  // before those of tile u + 1) so that each multiply waits for its own data.
-  __device__ __forceinline__ void issue(int t0, int cnt) {
-#pragma unroll
-    for (int u = 0; u < CT; u++) {
-      const uint32_t sb = (uint32_t)(t0 + u) * TB;
-      const uint32_t bo = u < cnt ? bvoff : FGM_OOB;
-#pragma unroll
-      for (int t = 0; t < 4; t++) braw[u][t] = buf_load_b32(rb, bo + t * (BITS == 8 ? 64u : 32u), sb);
-      if (HALF) {
-        if ((u & 1) == 0)
-          af[u >> 1][0] = buf_load_b128(ra, (u + h < cnt) ? avoff[0] : FGM_OOB, (uint32_t)(t0 + u) * 1024u);
-      } else {
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-          af[u][mb] = buf_load_b128(ra, u < cnt ? avoff[mb] : FGM_OOB, (uint32_t)(t0 + u) * 1024u);
-      }
-    }
-  }
+// Shape constants of a kernel variant.
+template <int BITS, int MB, bool HALF>
+struct Geo {
+  static constexpr int TPU = BITS == 4 ? 2 : 1;       // k-tiles per 1 KB unit
+  static constexpr int OUT = HALF ? 128 : 256 * MB;   // outputs per n-block
+  static constexpr int NA = HALF ? 1 : MB * TPU;      // activation loads per unit
+  static constexpr int X = 1 + NA;                    // vector-memory instructions per unit
+  static constexpr int D = ring_depth(BITS, MB, HALF);
+};
 
-  // int4: the finished group's sums into LDS
-  __device__ __forceinline__ void park(int grp) {
-    if (HALF) {
-      if (pb[0][0]) {  // lanes of rows 0-7
-#pragma unroll
-        for (int r = 0; r < 4; r++) pb[0][r][grp] = RAW ? acc[0][r] : __float_as_int((float)acc[0][r]);
-      }
-    } else {
-#pragma unroll
-      for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          if (pb[mb][r]) pb[mb][r][grp] = RAW ? acc[mb][r] : __float_as_int((float)acc[mb][r]);
-    }
-  }
-
-  // G1: one k-block per group (group 64), so tile u of a chunk is group gi + u
-  template <bool G1>
-  __device__ __forceinline__ void compute(int cnt) {
-#pragma unroll
-    for (int u = 0; u < CT; u++) {
-      if (u >= cnt) break;
-      v4i bv;
-#pragma unroll
-      for (int t = 0; t < 4; t++)
-        bv[t] = BITS == 8 ? braw[u][t] : (int)(((uint32_t)braw[u][t] << sh) & 0xF0F0F0F0u);
-      const bool fresh = BITS == 4 && (G1 || gpos == 0);
-      if (HALF) {
-        // lanes j >= 8 feed rows 8-15 of the product, which are never read:
-        // they keep whatever the other tile of the pair puts there
-        const v4i x = af[u >> 1][0];
-        v4i av;
-#pragma unroll
-        for (int q = 0; q < 4; q++) av[q] = (u & 1) ? ror8(x[q]) : x[q];
-        acc[0] = fresh ? mfma16(av, bv, v4i{0, 0, 0, 0}) : mfma16(av, bv, acc[0]);
-      } else {
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-          acc[mb] = fresh ? mfma16(af[u][mb], bv, v4i{0, 0, 0, 0}) : mfma16(af[u][mb], bv, acc[mb]);
-      }
-      if (BITS == 4) {
-        if (G1) {
-          park(gi + u);
-        } else if (++gpos == gk) {
-          park(gi++);
-          gpos = 0;
-        }
-      }
-    }
-    if (BITS == 4 && G1) gi += cnt;
+// LDS layout of one workgroup (bytes), shared by the host (sizing) and the
+// kernel: the weight rings (also the q8c reduction area afterwards), then
+// (int4) the parked tile sums of every k-tile ([n-block][output][k-tile],
+// pitch pp) and the group scales ([n-block][column][group], pitch ngp, zero
+// past the last group); then the epilogue scales.
+struct Lay {
+  uint32_t ring, park, scl, asc, bsc, total;
+  int slots, pp, ngp;
+  __host__ __device__ Lay(int bits, int out, int d, int ks, int upw, int nws, int nbw, int kb, int mp) {
+    const int tpu = bits == 4 ? 2 : 1;
+    slots = upw < d ? upw : d;
+    ring = 0;
+    uint32_t o = (uint32_t)nws * slots * 1024;
+    // int4: parked k-tiles (K rounded up to whole rounds) and scales padded
+    // to whole 4-tile chunks
+    pp = pitch4(tpu * ks * upw);
+    ngp = pitch4((kb + 3) / 4 * 4);
+    park = o;
+    o += bits == 4 ? (uint32_t)nbw * out * pp * 4 : 0;
+    scl = o;
+    o += bits == 4 ? (uint32_t)nbw * 16 * ngp * 4 : 0;
+    asc = o;
+    o += (uint32_t)(mp + 3) / 4 * 16;
+    bsc = o;
+    o += (uint32_t)nbw * 64;
+    total = o;
   }
 };
 
-template <int BITS, int MB, bool HALF, int CT, bool G1, bool RAW>
+template <int BITS, int MB, bool HALF, bool G1, bool RAW>
 __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
-  extern __shared__ __attribute__((aligned(16))) int32_t lds[];
+  using G = Geo<BITS, MB, HALF>;
+  constexpr int TPU = G::TPU, OUT = G::OUT, NA = G::NA, X = G::X, D = G::D;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick(bt);
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, NT = blockDim.x;
   const int w = wave_id(), l = tid & 63, g = l >> 4, j = l & 15;
   const int M = a.M, N = a.N, KB = a.K >> 6;
-  const int Mp = HALF ? 8 : M;  // rows of the parked sums
-  const int KS = a.ks, NBW = a.nbw, TW = a.tw;
-  const int gk = (BITS == 4) ? (a.group >> 6) : 1;
-  const int NG = (BITS == 4) ? KB / gk : 1;
-  const int NGP = group_pitch(NG);
+  const int KS = a.ks, NBW = a.nbw, UPW = a.tw;
+  const int NWS = NT >> 6, NWP = KS * NBW;         // waves, waves with an n-block
+  const int TR = TPU * KS;                         // k-tiles per round
+  const int gk = BITS == 4 ? a.group >> 6 : 1;
+  const int NG = BITS == 4 ? KB / gk : 0;
+  const int Mp = HALF ? 8 : 16 * MB;
   const int nb_first = a.n0 + (int)(blockIdx.x - a.wg0) * NBW;
-  const int nb_here = min(NBW, a.n0 + a.nblocks - nb_first);  // n-blocks in this workgroup
-  const int nbi = w / KS, s = w - nbi * KS;                    // wave-uniform
-  const bool want_scales = BITS == 4 && !RAW;
-  const int psz = Mp * 16 * NGP;                                // parked words per n-block
+  const int nb_here = min(NBW, a.n0 + a.nblocks - nb_first);
+  const Lay L(BITS, OUT, D, KS, UPW, NWS, NBW, KB, Mp);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+  constexpr uint32_t TB = BITS == 4 ? 512u : 1024u;  // bytes per k-tile
 
-  // 1. the first chunk of this wave's weight stream
-  Stream<BITS, MB, HALF, CT, RAW> st;
-  const bool streaming = nbi < nb_here;
-  const int tb = s * TW, te = min(KB, tb + TW);
-  if (streaming) {
-    const int nb = nb_first + nbi;
-    st.rb = make_rsrc((const int8_t*)a.B + (size_t)nb * KB * st.TB, (uint32_t)KB * st.TB);
-    st.ra = make_rsrc(a.A, (uint32_t)((M + 15) / 16 * KB * 1024));
-    st.h = j >> 3;
-    st.sh = j < 8 ? 4 : 0;
-    st.bvoff = BITS == 8 ? (uint32_t)(256 * g + 4 * j) : (uint32_t)(128 * g + 4 * (j & 7));
-    if (HALF) {
-      const int r = j & 7;
-      st.avoff[0] = r < M ? (uint32_t)(st.h * 1024 + r * 64 + 16 * g) : FGM_OOB;
-    } else {
-#pragma unroll
-      for (int mb = 0; mb < MB; mb++)
-        st.avoff[mb] = (mb * 16 + j < M) ? (uint32_t)(mb * KB * 1024 + j * 64 + 16 * g) : FGM_OOB;
-    }
+  // ---- the stream: this wave's weights (an empty range if it has no
+  // n-block), packed A
+  const int q = w / KS, s = w - q * KS;            // wave's n-block, K slice
+  const bool live = w < NWP && q < nb_here;
+  const int UPWw = w < NWP ? UPW : 0;              // units this wave streams
+  const v4i rb = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (live ? q : 0)) * KB * TB,
+                            live ? (uint32_t)KB * TB : 0u);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, (uint32_t)((M + 15) / 16) * KB * 1024);
+  const uint32_t bsw = BITS == 4 ? 16u * (uint32_t)(l ^ (((l >> 3) & 3) << 1))
+                                 : 16u * (uint32_t)(l ^ (((l >> 4) & 3) << 2));
+  uint32_t avoff[NA];
+  if (HALF) {
+    const int r = j & 7;
+    const bool ok = r < M && (BITS == 4 || j < 8);
+    avoff[0] = ok ? (uint32_t)((j >> 3) * 1024 + r * 64 + 16 * g) : FGM_OOB;
+  } else {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = mb * 16 + 4 * g + r;
-        st.pb[mb][r] = m < Mp ? lds + (size_t)nbi * psz + (size_t)(m * 16 + j) * NGP : nullptr;
-      }
-    st.gk = gk;
-    st.gpos = 0;
-    st.gi = tb / gk;
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) st.acc[mb] = v4i{0, 0, 0, 0};
-    st.issue(tb, min(CT, te - tb));
+      for (int e = 0; e < TPU; e++)
+        avoff[mb * TPU + e] = (16 * mb + j < M) ? (uint32_t)(mb * KB * 1024 + e * 1024 + j * 64 + 16 * g)
+                                                : FGM_OOB;
   }
+  const uint32_t ring_w = lds0 + L.ring + (uint32_t)w * L.slots * 1024;
 
-  // 2. group scales of this workgroup's columns, two columns per dword, in
-  //    flight behind the weights.  NBW is a power of two; dword i holds group
-  //    i >> lg, columns 16 * nb_first + 2 * (i & (8 * NBW - 1)) + {0, 1}.
-  const int lg = __builtin_ctz(NBW) + 3;
-  const int nsd = NG << lg;  // host: <= SPT * blockDim
-  uint32_t sreg[SPT];
-  if (want_scales) {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.b_scale, (uint32_t)NG * N * 2);
+  // one DMA of 1 KB of weights into ring slot sl, and the activation
+  // fragments of the same k-tiles into af[sl]
+  v4i af[D][NA];
+  auto issue = [&](int u, auto slc) __attribute__((always_inline)) {
+    constexpr int sl = decltype(slc)::value;
+    const uint32_t gu = (uint32_t)(u * KS + s);    // unit index in the n-block
+    dma16<true>(rb, ring_w + sl * 1024, bsw, gu * 1024u);
 #pragma unroll
-    for (int u = 0; u < SPT; u++) {
-      const int i = tid + u * (int)blockDim.x;
-      const int gi = i >> lg, c2 = i & ((1 << lg) - 1);
-      const bool ok = i < nsd && (c2 >> 3) < nb_here;
-      sreg[u] = (uint32_t)buf_load_b32(rs, ok ? (uint32_t)((gi * N + nb_first * 16 + 2 * c2) * 2) : FGM_OOB, 0);
+    for (int x = 0; x < NA; x++) af[sl][x] = buf_load_b128(ra, avoff[x], gu * TPU * 1024u);
+  };
+  // units 0 .. D - 2 in flight
+  sfor<0, D - 1>([&](auto ic) {
+    if (decltype(ic)::value < UPWw) issue(decltype(ic)::value, ic);
+  });
+
+  // ---- PRE: epilogue scales, after the first units (the stream starts
+  // first); they are only read after the stream
+  constexpr int PRE = (BITS == 4 && !RAW ? SPT : 0) + (RAW ? 0 : (BITS == 8 ? 2 : 1));
+  uint32_t sreg[SPT];
+  float rscale = 0.0f, cscale = 0.0f;
+  if (BITS == 4 && !RAW) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.b_scale, (uint32_t)NG * N * 2);
+    const int per_g = 8 * NBW;  // dwords per group (two columns each)
+#pragma unroll
+    for (int v = 0; v < SPT; v++) {
+      const int i = tid + v * NT, gi = i / per_g, c2 = i - gi * per_g, qq = c2 >> 3;
+      const bool ok = gi < NG && qq < nb_here;
+      sreg[v] = (uint32_t)buf_load_b32(rs, ok ? (uint32_t)((gi * N + (nb_first + qq) * 16 + 2 * (c2 & 7)) * 2) : FGM_OOB, 0);
     }
   }
-
-  // per-row activation scales, and (int8) per-column weight scales of this
-  // workgroup, for the epilogue
-  float rscale = 0.0f, cscale = 0.0f;
   if (!RAW) {
     const __amdgpu_buffer_rsrc_t ras = make_rsrc(a.a_scale, (uint32_t)M * 4);
     rscale = __int_as_float(buf_load_b32(ras, tid < M ? (uint32_t)tid * 4 : FGM_OOB, 0));
     if (BITS == 8) {
       const __amdgpu_buffer_rsrc_t rbs = make_rsrc(a.b_scale, (uint32_t)N * 4);
-      const int col = nb_first * 16 + tid;
-      cscale = __int_as_float(buf_load_b32(rbs, tid < nb_here * 16 ? (uint32_t)col * 4 : FGM_OOB, 0));
+      cscale = __int_as_float(
+          buf_load_b32(rbs, tid < nb_here * 16 ? (uint32_t)(nb_first * 16 + tid) * 4 : FGM_OOB, 0));
     }
   }
 
-  // 3. the multiplies, then the rest of the stream (waves with more than CT
-  //    k-blocks: long K, or groups wider than CT k-blocks)
-  if (streaming) {
-    st.template compute<G1>(min(CT, te - tb));
-    for (int t0 = tb + CT; t0 < te; t0 += CT) {
-      st.issue(t0, min(CT, te - t0));
-      st.template compute<G1>(min(CT, te - t0));
-    }
-    if (BITS == 8) {
-      int32_t* R = lds + (size_t)w * Mp * 16;
+  // per-lane B fragment offsets within a unit (tile e adds 512 for int4)
+  uint32_t boff[4];
 #pragma unroll
-      for (int mb = 0; mb < MB; mb++)
+  for (int t = 0; t < 4; t++) {
+    const int c = BITS == 4 ? ((8 * g + 2 * t + ((j & 7) >> 2)) ^ (g << 1))
+                            : ((16 * g + 4 * t + (j >> 2)) ^ (g << 2));
+    boff[t] = 16u * (uint32_t)c + 4u * (uint32_t)(j & 3);
+  }
+  const int sh = j < 8 ? 4 : 0;
+  v4i acc[MB];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int m = mb * 16 + 4 * g + r;
-          if (m < Mp) R[m * 16 + j] = st.acc[mb][r];
+  for (int mb = 0; mb < MB; mb++) acc[mb] = v4i{0, 0, 0, 0};
+  const int npro = min(D - 1, UPWw);             // units issued before PRE
+
+  for (int u0 = 0; u0 < UPWw; u0 += D) {
+    sfor<0, D>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int u = u0 + i;
+      if (u < UPWw) {
+        // unit u landed: min(D - 2, UPW - 1 - u) later units, and PRE if
+        // it was issued after unit u, may still be in flight
+        const int later = min(D - 2, UPWw - 1 - u);
+        if (u < npro) {
+          sfor<0, D - 1>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            if (later == k) wait_vm<k * X + PRE>();
+          });
+        } else {
+          sfor<0, D - 1>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            if (later == k) wait_vm<k * X>();
+          });
         }
-    }
-  }
-
-  // int4 scales in LDS as f32 / 16 (exact): [n-block][column][group], pitch NGP
-  float* SF = (float*)(lds + (size_t)NBW * psz);
-  if (want_scales) {
+        // B fragments of unit u
+        const char* slot = smem + L.ring + ((size_t)w * L.slots + i) * 1024;
+        v4i bv[TPU];
 #pragma unroll
-    for (int u = 0; u < SPT; u++) {
-      const int i = tid + u * (int)blockDim.x;
-      const int gi = i >> lg, c2 = i & ((1 << lg) - 1);
-      if (i < nsd && (c2 >> 3) < nb_here) {
-        const int q = c2 >> 3, c = 2 * (c2 & 7);
-        float* d = SF + ((size_t)q * 16 + c) * NGP + gi;
-        d[0] = f16_bits_to_f32((uint16_t)(sreg[u] & 0xFFFF)) * 0.0625f;
-        d[NGP] = f16_bits_to_f32((uint16_t)(sreg[u] >> 16)) * 0.0625f;
+        for (int e = 0; e < TPU; e++)
+#pragma unroll
+          for (int t = 0; t < 4; t++) {
+            const uint32_t x = *(const uint32_t*)(slot + e * 512 + boff[t]);
+            bv[e][t] = BITS == 8 ? (int)x : (int)((x << sh) & 0xF0F0F0F0u);
+          }
+        // refill the slot consumed one step ago
+        if (u + D - 1 < UPWw) issue(u + D - 1, std::integral_constant<int, (i + D - 1) % D>{});
+        if (BITS == 8) {
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++) acc[mb] = mfma16(af[i][HALF ? 0 : mb], bv[0], acc[mb]);
+        } else {
+          v4i ts[TPU][MB];  // tile sums (16 * acc)
+          if (HALF) {
+            const v4i x = af[i][0];
+            v4i x1;
+#pragma unroll
+            for (int d = 0; d < 4; d++) x1[d] = ror8(x[d]);
+            ts[0][0] = mfma16(x, bv[0], v4i{0, 0, 0, 0});
+            ts[1][0] = mfma16(x1, bv[1], v4i{0, 0, 0, 0});
+          } else {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+              for (int e = 0; e < TPU; e++) ts[e][mb] = mfma16(af[i][mb * TPU + e], bv[e], v4i{0, 0, 0, 0});
+          }
+          // park [n-block][output][k-tile], k-tile TR u + 2 s + e
+          int32_t* P = (int32_t*)(smem + L.park) + (q * OUT) * L.pp + TR * u + 2 * s;
+          if (!HALF || g < 2) {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+              for (int r = 0; r < 4; r++) {
+                const int oo = (16 * mb + 4 * g + r) * 16 + j;
+                // group 64: the sum is a whole group's, parked as the float
+                // the chain multiplies (exact: |16 acc| < 2^24)
+                if (G1 && !RAW)
+                  *(float2*)(P + oo * L.pp) = float2{(float)ts[0][mb][r], (float)ts[1][mb][r]};
+                else
+                  *(int2*)(P + oo * L.pp) = int2{ts[0][mb][r], ts[1][mb][r]};
+              }
+          }
+        }
+      }
+    });
+  }
+  wait_vm<0>();  // the stream and PRE landed; no DMA still writes the ring
+
+  float* ASC = (float*)(smem + L.asc);
+  if (!RAW && tid < M) ASC[tid] = rscale;
+
+  if (BITS == 4) {
+    // ---- q4g: group scales into LDS as f32 / 16, zero past the last group
+    // (padded k-tiles add +0); then one thread per output runs its chain
+    float* S = (float*)(smem + L.scl);
+    if (!RAW) {
+      const int per_g = 8 * NBW;
+#pragma unroll
+      for (int v = 0; v < SPT; v++) {
+        const int ii = tid + v * NT, gi = ii / per_g, c2 = ii - gi * per_g, qq = c2 >> 3;
+        if (gi < L.ngp && qq < NBW) {
+          float* d = S + (qq * 16 + 2 * (c2 & 7)) * L.ngp + gi;
+          const bool ok = gi < NG && qq < nb_here;
+          d[0] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] & 0xFFFF)) * 0.0625f : 0.0f;
+          d[L.ngp] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] >> 16)) * 0.0625f : 0.0f;
+        }
       }
     }
+    __syncthreads();
+    for (int o = tid; o < NBW * OUT; o += NT) {
+      const int qq = o / OUT, oo = o - qq * OUT, m = oo >> 4, c = oo & 15;
+      if (qq >= nb_here || m >= M) continue;
+      const int32_t* P = (const int32_t*)(smem + L.park) + (qq * OUT + oo) * L.pp;
+      const float* Sc = S + (qq * 16 + c) * L.ngp;
+      const int n = (nb_first + qq) * 16 + c;
+      if (G1 && !RAW) {
+        // group = k-tile: chunks of four; the next chunk's sums and scales are
+        // read (volatile: kept in place) before this chunk's fmas
+        // LDS reads by address (ds_read_b128 in inline asm, waited for with
+        // lgkmcnt): the compiler would otherwise sink the prefetch next to
+        // its use.  The sums are parked as floats.  Reads up to three chunks
+        // past a row stay inside the workgroup's LDS and are not used.
+        const uint32_t pa0 = lds0 + L.park + (uint32_t)((qq * OUT + oo) * L.pp) * 4u;
+        const uint32_t sa0 = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
+        const int nch = (KB + 3) >> 2;           // k-tiles past K hold zeros
+        float cacc = 0.0f;
+        v4i pv[4], sv[4];
+        lds_read2x128<0>(pv[0], sv[0], pa0, sa0);
+        lds_read2x128<16>(pv[1], sv[1], pa0, sa0);
+        lds_read2x128<32>(pv[2], sv[2], pa0, sa0);
+        for (int ch = 0; ch < nch; ch += 4) {
+          const uint32_t pb = pa0 + 16u * ch, sb = sa0 + 16u * ch;
+          sfor<0, 4>([&](auto bc) {
+            constexpr int b = decltype(bc)::value;
+            lds_read2x128<16 * (b + 3)>(pv[(b + 3) & 3], sv[(b + 3) & 3], pb, sb);
+            lgkm_wait6(pv[b], sv[b]);
+            if (ch + b < nch) {
+              cacc = __builtin_fmaf(__int_as_float(pv[b].x), __int_as_float(sv[b].x), cacc);
+              cacc = __builtin_fmaf(__int_as_float(pv[b].y), __int_as_float(sv[b].y), cacc);
+              cacc = __builtin_fmaf(__int_as_float(pv[b].z), __int_as_float(sv[b].z), cacc);
+              cacc = __builtin_fmaf(__int_as_float(pv[b].w), __int_as_float(sv[b].w), cacc);
+            }
+          });
+        }
+        sfor<0, 4>([&](auto bc) { lgkm_wait0(pv[decltype(bc)::value], sv[decltype(bc)::value]); });
+        a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
+      } else {
+        // any group size, and the raw per-group sums
+        float cacc = 0.0f;
+        int gsum = 0;
+        for (int kt = 0; kt < KB; kt++) {
+          gsum += P[kt];
+          if ((kt + 1) % gk == 0) {
+            if (RAW) a.acc_out[((size_t)(kt / gk) * M + m) * a.ldacc + n] = gsum >> 4;
+            else cacc = __builtin_fmaf((float)gsum, Sc[kt / gk], cacc);
+            gsum = 0;
+          }
+        }
+        if (!RAW) a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
+      }
+    }
+    return;
   }
-  // epilogue scales: a_scale [Mp], then (int8) b_scale [NBW * 16]
-  float* ASC = BITS == 4 ? SF + (size_t)NBW * 16 * NGP : (float*)(lds + (size_t)(blockDim.x >> 6) * Mp * 16);
-  float* BSC = ASC + Mp;
-  if (!RAW) {
-    if (tid < M) ASC[tid] = rscale;
-    if (BITS == 8 && tid < nb_here * 16) BSC[tid] = cscale;
+
+  // ---- q8c: the KS partial sums of an n-block, added in LDS (the ring is
+  // free now)
+  float* BSC = (float*)(smem + L.bsc);
+  if (!RAW && tid < nb_here * 16) BSC[tid] = cscale;
+  __syncthreads();
+  int32_t* R = (int32_t*)(smem + L.ring);
+  if (w < NWP && (!HALF || g < 2)) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) R[w * OUT + (16 * mb + 4 * g + r) * 16 + j] = acc[mb][r];
   }
   __syncthreads();
-
-  // 4. epilogue: one thread per output of the workgroup's n-blocks
-  const int per_nb = Mp * 16;
-  for (int o = tid; o < nb_here * per_nb; o += blockDim.x) {
-    const int q = o / per_nb, rem = o - q * per_nb;
-    const int m = rem >> 4, c = rem & 15;
-    if (m >= M) continue;
-    const int ncol = (nb_first + q) * 16 + c;
-    if (BITS == 8) {
-      int32_t sum = 0;
-      for (int ss = 0; ss < KS; ss++) sum += lds[((size_t)(q * KS + ss) * Mp + m) * 16 + c];
-      if (RAW) {
-        a.acc_out[(size_t)m * a.ldacc + ncol] = sum;
-      } else {
-        const float sc = BSC[q * 16 + c] * ASC[m];
-        a.C[(size_t)m * a.ldc + ncol] = (float)sum * sc;
-      }
-    } else {
-      const int32_t* pr = lds + (size_t)q * psz + (size_t)(m * 16 + c) * NGP;
-      if (RAW) {
-        for (int gg = 0; gg < NG; gg++) a.acc_out[((size_t)gg * M + m) * a.ldacc + ncol] = pr[gg] >> 4;
-      } else {
-        // the chain is serial: four groups per 16-byte read of the sums and
-        // of the scales, the reads of the next quad issued before the fmas
-        const float* pf = (const float*)pr;
-        const float* sr = SF + ((size_t)q * 16 + c) * NGP;
-        const int nq = NG >> 2;
-        float cacc = 0.0f;
-        if (nq > 0) {
-          float4 pv = *(const float4*)pf, sv = *(const float4*)sr;
-          for (int qq = 1; qq < nq; qq++) {
-            const float4 pn = *(const float4*)(pf + 4 * qq), sn = *(const float4*)(sr + 4 * qq);
-            cacc = __builtin_fmaf(pv.x, sv.x, cacc);
-            cacc = __builtin_fmaf(pv.y, sv.y, cacc);
-            cacc = __builtin_fmaf(pv.z, sv.z, cacc);
-            cacc = __builtin_fmaf(pv.w, sv.w, cacc);
-            pv = pn;
-            sv = sn;
-          }
-          cacc = __builtin_fmaf(pv.x, sv.x, cacc);
-          cacc = __builtin_fmaf(pv.y, sv.y, cacc);
-          cacc = __builtin_fmaf(pv.z, sv.z, cacc);
-          cacc = __builtin_fmaf(pv.w, sv.w, cacc);
-        }
-        for (int gg = 4 * nq; gg < NG; gg++) cacc = __builtin_fmaf(pf[gg], sr[gg], cacc);
-        a.C[(size_t)m * a.ldc + ncol] = cacc * ASC[m];
-      }
-    }
+  for (int o = tid; o < NBW * OUT; o += NT) {
+    const int qq = o / OUT, oo = o - qq * OUT, m = oo >> 4, c = oo & 15;
+    if (qq >= nb_here || m >= M) continue;
+    int32_t sum = 0;
+    for (int ss = 0; ss < KS; ss++) sum += R[(qq * KS + ss) * OUT + oo];
+    const int n = (nb_first + qq) * 16 + c;
+    if (RAW) a.acc_out[(size_t)m * a.ldacc + n] = sum;
+    else a.C[(size_t)m * a.ldc + n] = (float)sum * (BSC[qq * 16 + c] * ASC[m]);
   }
 }
 
-// Tiles per chunk: about 4 KB of weights per wave, fewer with more m-blocks
-// (each tile then needs MB activation fragments in registers).
-#ifndef FGM_CT4
-#define FGM_CT4 8
-#endif
-constexpr int ct_for(int bits, int MB) {
-  return bits == 4 ? (MB == 1 ? FGM_CT4 : (MB == 2 ? 4 : 2)) : (MB == 1 ? 4 : (MB == 2 ? 2 : 1));
+int pow2ceil(int x) {
+  int p = 1;
+  while (p < x) p *= 2;
+  return p;
+}
+
+// K split of one GEMM: KS stream waves per n-block (a power of two), each
+// with UPW units of 1 KB.
+void plan_split(int bits, int M, int K, int* ks, int* upw) {
+  const int KB = K / 64, tpu = bits == 4 ? 2 : 1;
+  const int kbu = (KB + tpu - 1) / tpu;
+  int k = pow2ceil((kbu + FGM_DEC_UPW - 1) / FGM_DEC_UPW);
+  if (k > MAX_WAVES) k = MAX_WAVES;
+  *ks = k;
+  *upw = (kbu + k - 1) / k;
+}
+
+Lay lay_for(int bits, int M, int K, int ks, int nws, int nbw) {
+  const int MB = (M + 15) / 16;
+  const bool half = M <= 8;
+  const int out = half ? 128 : 256 * MB;
+  const int tpu = bits == 4 ? 2 : 1;
+  const int upw = ((K / 64 + tpu - 1) / tpu + ks - 1) / ks;
+  return Lay(bits, out, ring_depth(bits, MB, half), ks, upw, nws, nbw, K / 64, half ? 8 : 16 * MB);
+}
+
+// Does one problem fit a workgroup of nws waves with nbw n-blocks?
+bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw) {
+  if (ks * nbw > nws || nws > MAX_WAVES) return false;
+  const Lay L = lay_for(bits, M, K, ks, nws, nbw);
+  if (bits == 4) {
+    // the group-scale prefetch covers every padded group slot
+    if (8 * nbw * L.ngp > SPT * 64 * nws) return false;
+    (void)group;
+  } else {
+    // the q8c reduction reuses the rings
+    const int out = M <= 8 ? 128 : 256 * ((M + 15) / 16);
+    if ((size_t)nws * out * 4 > (size_t)nws * L.slots * 1024) return false;
+  }
+  return L.total <= 160 * 1024;
 }
 
 template <int BITS, int MB, bool HALF, bool G1, bool RAW>
-hipError_t launch_variant(const GemmBatch& bt, int W, size_t lds, int nwg, hipStream_t st) {
-  constexpr int CT = ct_for(BITS, MB);
-  auto k = decode_kernel<BITS, MB, HALF, CT, G1, RAW>;
+hipError_t launch_variant(const GemmBatch& bt, int nw, size_t lds, int nwg, hipStream_t st) {
+  auto k = decode_kernel<BITS, MB, HALF, G1, RAW>;
   static hipError_t attr = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(k, dim3(nwg), dim3(W * 64), lds, st, bt);
+  hipLaunchKernelGGL(k, dim3(nwg), dim3(nw * 64), lds, st, bt);
   return hipGetLastError();
 }
 
 template <int BITS, int MB, bool HALF>
-hipError_t launch_decode(const GemmBatch& bt, bool g1, bool raw, int W, size_t lds, int nwg, hipStream_t st) {
+hipError_t launch_decode(const GemmBatch& bt, bool g1, bool raw, int nw, size_t lds, int nwg, hipStream_t st) {
   if constexpr (BITS == 8) {
-    return raw ? launch_variant<BITS, MB, HALF, false, true>(bt, W, lds, nwg, st)
-               : launch_variant<BITS, MB, HALF, false, false>(bt, W, lds, nwg, st);
+    return raw ? launch_variant<BITS, MB, HALF, false, true>(bt, nw, lds, nwg, st)
+               : launch_variant<BITS, MB, HALF, false, false>(bt, nw, lds, nwg, st);
   }
-  if (raw) return g1 ? launch_variant<BITS, MB, HALF, true, true>(bt, W, lds, nwg, st)
-                     : launch_variant<BITS, MB, HALF, false, true>(bt, W, lds, nwg, st);
-  return g1 ? launch_variant<BITS, MB, HALF, true, false>(bt, W, lds, nwg, st)
-            : launch_variant<BITS, MB, HALF, false, false>(bt, W, lds, nwg, st);
-}
-
-// K split of one GEMM: TW k-blocks per wave (a multiple of the group's
-// k-blocks), KS = ceil(KB / TW) <= MAX_WAVES waves per n-block.
-void plan_split(int bits, int M, int K, int group, int* tw, int* ks) {
-  const int KB = K / 64, MB = (M + 15) / 16;
-  const int gk = bits == 4 ? group / 64 : 1;
-  const int ct = ct_for(bits, MB);
-  int t = ct >= gk ? (ct / gk) * gk : gk;
-  int s = (KB + t - 1) / t;
-  if (s > MAX_WAVES) {
-    t = (KB + MAX_WAVES - 1) / MAX_WAVES;
-    t = (t + gk - 1) / gk * gk;
-    s = (KB + t - 1) / t;
-  }
-  *tw = t;
-  *ks = s;
-}
-
-size_t lds_need(int bits, int M, int K, int group, int nbw, int W) {
-  const int Mp = M <= 8 ? 8 : M;
-  const size_t esc = (size_t)Mp + (size_t)nbw * 16;  // epilogue scales
-  if (bits == 4) {
-    const int NG = (K / 64) / (group / 64);
-    return ((size_t)nbw * (Mp + 1) * 16 * group_pitch(NG) + esc) * 4;
-  }
-  return ((size_t)W * Mp * 16 + esc) * 4;
+  if (raw) return launch_variant<BITS, MB, HALF, false, true>(bt, nw, lds, nwg, st);
+  return g1 ? launch_variant<BITS, MB, HALF, true, false>(bt, nw, lds, nwg, st)
+            : launch_variant<BITS, MB, HALF, false, false>(bt, nw, lds, nwg, st);
 }
 
 }  // namespace
 
 bool fgm_decode_fits(int bits, int M, int K, int group) {
+  (void)group;
   if (M < 1 || M > 64) return false;
   if ((size_t)((M + 15) / 16) * K * 16 > 0x7FFFFFFFu) return false;  // buffer offsets
-  int tw, ks;
-  plan_split(bits, M, K, group, &tw, &ks);
-  if (bits == 4) {
-    const int NG = (K / 64) / (group / 64);
-    if (NG * 8 > SPT * 64 * ks) return false;  // scale prefetch of one n-block
-  }
-  return lds_need(bits, M, K, group, 1, ks) <= 160 * 1024;
+  int ks, upw;
+  plan_split(bits, M, K, &ks, &upw);
+  const int nws = ks < FGM_DEC_NWMIN ? FGM_DEC_NWMIN : ks;
+  return fits_wg(bits, M, K, group, nws, ks, 1);
 }
 
 size_t fgm_decode_lds_bytes(int bits, int M, int K, int group) {
-  int tw, ks;
-  plan_split(bits, M, K, group, &tw, &ks);
-  return lds_need(bits, M, K, group, 1, ks);
+  (void)group;
+  int ks, upw;
+  plan_split(bits, M, K, &ks, &upw);
+  const int nws = ks < FGM_DEC_NWMIN ? FGM_DEC_NWMIN : ks;
+  return lay_for(bits, M, K, ks, nws, 1).total;
 }
 
-// Every problem of the batch gets the same workgroup size W = the largest
-// K split; a problem with a smaller split packs W / KS n-blocks into each
-// workgroup, as far as LDS and the scale prefetch allow.
+// Every problem of the batch gets the same number of stream waves NWS = the
+// largest K split (at least FGM_DEC_NWMIN); a problem with a smaller split
+// packs NWS / KS n-blocks into each workgroup, as far as LDS and the scale
+// prefetch allow (waves without an n-block only take part in the barriers).
 hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   // one kernel variant per launch: split a batch that mixes raw-accumulator
   // and scaled problems, or (int4) group 64 with wider groups
@@ -440,8 +533,7 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
       return e != hipSuccess ? e : fgm_launch_decode(bits, b, st);
     }
   }
-  // problems with the longest K first: their workgroups are dispatched
-  // first, and their epilogue chains are the longest
+  // problems with the longest K first: their workgroups are dispatched first
   GemmBatch bt = in;
   for (int i = 1; i < bt.count; i++)
     for (int k = i; k > 0 && bt.p[k].K > bt.p[k - 1].K; k--) {
@@ -449,52 +541,52 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
       bt.p[k] = bt.p[k - 1];
       bt.p[k - 1] = t;
     }
-  int W = 1, MB = 0, Mmax = 0;
+  int NWS = FGM_DEC_NWMIN, MB = 0, Mmax = 0;
   for (int i = 0; i < bt.count; i++) {
     GemmProb& p = bt.p[i];
-    plan_split(bits, p.M, p.K, p.group, &p.tw, &p.ks);
-    if (p.ks > W) W = p.ks;
+    plan_split(bits, p.M, p.K, &p.ks, &p.tw);
+    if (p.ks > NWS) NWS = p.ks;
     const int mb = (p.M + 15) / 16;
     if (mb > MB) MB = mb;
     if (p.M > Mmax) Mmax = p.M;
   }
+  const bool half = MB == 1 && Mmax <= 8;
+  const int Mv = half ? 8 : 16 * MB;  // the variant's row blocking
   int nwg = 0;
   size_t lds = 0;
   for (int i = 0; i < bt.count; i++) {
     GemmProb& p = bt.p[i];
-    // a power of two (the kernel maps scale dwords with shifts)
-    int nbw = 1;
-    while (nbw * 2 * p.ks <= W && nbw * 2 <= p.nblocks) nbw *= 2;
-    while (nbw > 1 && lds_need(bits, p.M, p.K, p.group, nbw, W) > 160 * 1024) nbw /= 2;
-    if (bits == 4) {
-      const int NG = (p.K / 64) / (p.group / 64);
-      while (nbw > 1 && nbw * NG * 8 > SPT * 64 * W) nbw /= 2;
-    }
+    int nbw = NWS / p.ks;
+    while (nbw > 1 && (nbw > p.nblocks || !fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw))) nbw /= 2;
+    if (!fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw)) return hipErrorInvalidValue;
     p.nbw = nbw;
     p.wg0 = nwg;
     nwg += (p.nblocks + nbw - 1) / nbw;
-    const size_t need = lds_need(bits, p.M, p.K, p.group, nbw, W);
+    const size_t need = lay_for(bits, Mv, p.K, p.ks, NWS, nbw).total;
     if (need > lds) lds = need;
   }
   if (nwg == 0) return hipSuccess;
-  const bool half = MB == 1 && Mmax <= 8;
+  // the kernel derives a problem's stream waves as KS * NBW; pad the others
+  // up to the launch's NWS with idle n-blocks is not needed: every problem
+  // uses NBW = NWS / KS unless its n-blocks run out
+  const int NW = NWS;
   const bool g1 = bits == 4 && bt.p[0].group == 64;
   const bool raw = bt.p[0].acc_out != nullptr;
   if (bits == 8) {
-    if (half) return launch_decode<8, 1, true>(bt, g1, raw, W, lds, nwg, st);
+    if (half) return launch_decode<8, 1, true>(bt, g1, raw, NW, lds, nwg, st);
     switch (MB) {
-      case 1: return launch_decode<8, 1, false>(bt, g1, raw, W, lds, nwg, st);
-      case 2: return launch_decode<8, 2, false>(bt, g1, raw, W, lds, nwg, st);
-      case 3: return launch_decode<8, 3, false>(bt, g1, raw, W, lds, nwg, st);
-      case 4: return launch_decode<8, 4, false>(bt, g1, raw, W, lds, nwg, st);
+      case 1: return launch_decode<8, 1, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 2: return launch_decode<8, 2, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 3: return launch_decode<8, 3, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 4: return launch_decode<8, 4, false>(bt, g1, raw, NW, lds, nwg, st);
     }
   } else {
-    if (half) return launch_decode<4, 1, true>(bt, g1, raw, W, lds, nwg, st);
+    if (half) return launch_decode<4, 1, true>(bt, g1, raw, NW, lds, nwg, st);
     switch (MB) {
-      case 1: return launch_decode<4, 1, false>(bt, g1, raw, W, lds, nwg, st);
-      case 2: return launch_decode<4, 2, false>(bt, g1, raw, W, lds, nwg, st);
-      case 3: return launch_decode<4, 3, false>(bt, g1, raw, W, lds, nwg, st);
-      case 4: return launch_decode<4, 4, false>(bt, g1, raw, W, lds, nwg, st);
+      case 1: return launch_decode<4, 1, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 2: return launch_decode<4, 2, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 3: return launch_decode<4, 3, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 4: return launch_decode<4, 4, false>(bt, g1, raw, NW, lds, nwg, st);
     }
   }
   return hipErrorInvalidValue;

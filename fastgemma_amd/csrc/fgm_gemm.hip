@@ -54,54 +54,6 @@ FGM_DEV v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-// A raw buffer descriptor as four scalars (gfx9 layout: base, stride 0,
-// num_records, the same flags as make_rsrc).
-FGM_DEV v4i rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
-             __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xFFFF)),
-             __builtin_amdgcn_readfirstlane((int)bytes), FGM_BUF_FLAGS};
-}
-
-// One 16-byte chunk per lane from buffer offset voff + soff to LDS byte
-// address lds + 16 * lane (buffer_load_dwordx4 ... lds).  Out-of-range lanes
-// read zeros.  The compiler does not see these loads: the caller waits for
-// them with wait_vm.
-FGM_DEV void dma16(v4i rs, uint32_t lds, uint32_t voff, uint32_t soff) {
-  // lds and soff are wave-uniform: keep them in scalar registers
-  const int l0 = __builtin_amdgcn_readfirstlane((int)lds);
-  const int s0 = __builtin_amdgcn_readfirstlane((int)soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(l0), "v"(voff), "s"(rs), "s"(s0)
-               : "memory", "m0");
-}
-
-// One dword per lane to LDS byte address lds + 4 * lane (buffer_load_dword ...
-// lds); like dma16, waited for with wait_vm.
-FGM_DEV void dma4(v4i rs, uint32_t lds, uint32_t voff, uint32_t soff) {
-  const int l0 = __builtin_amdgcn_readfirstlane((int)lds);
-  const int s0 = __builtin_amdgcn_readfirstlane((int)soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :
-               : "s"(l0), "v"(voff), "s"(rs), "s"(s0)
-               : "memory", "m0");
-}
-
-template <int N>
-FGM_DEV void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
-// Compile-time loop: f(integral_constant<I>) for I = B .. E - 1.
-template <int B, int E, class F>
-FGM_DEV void sfor(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    sfor<B + 1, E>(f);
-  }
-}
-
 // Row position of weight-tile row r in the int8 LDS layout (an involution).
 FGM_DEV int rho(int r) { return (r & ~3) | ((r + 2 * ((r >> 2) & 1)) & 3); }
 
