@@ -357,6 +357,56 @@ def extra_cfg5(gpu):
     return {"workload": "long prefill M=2048 (gate/up int4 g64, down int8)", "per_shape": res}
 
 
+def extra_elem(gpu):
+    """The elementwise primitives between the GEMMs (rmsnorm, gelu_mul, rope,
+    add, softcap), at the model's decode (M=8) and prefill (M=256, 2048)
+    shapes, hidden 2048, FFN 8192, 8 heads x 256, logits 262144.  HBM-bound;
+    bytes = reads + writes of f32 operands."""
+    import numpy as np
+    from fastgemma_amd import kernels
+    t = gpu.t
+    L, F = gpu.L, gpu.F
+    res = {}
+
+    def rec(name, fn, nbytes, n=24):
+        dt = kernel_avg(gpu, fn, n, 3)
+        res[name] = {"us": dt * 1e6, "GB_s": nbytes / dt / 1e9, "frac_hbm": nbytes / dt / HBM_PEAK,
+                     "bytes": nbytes}
+
+    for M in (8, 256, 2048):
+        x = t.randn(M, 2048, device=gpu.dev)
+        w = t.randn(2048, device=gpu.dev)
+        o = t.empty_like(x)
+        rec(f"rmsnorm M={M} n=2048",
+            lambda i: F.check(L.fgm_hip_rmsnorm_dev(o.data_ptr(), x.data_ptr(), w.data_ptr(), M, 2048,
+                                                    1e-6, gpu.stream())),
+            8 * M * 2048 + 4 * 2048)
+        g = t.randn(M * 8192, device=gpu.dev)
+        u = t.randn(M * 8192, device=gpu.dev)
+        go = t.empty_like(g)
+        rec(f"gelu_mul M={M} n=8192",
+            lambda i: F.check(L.fgm_hip_gelu_mul_dev(go.data_ptr(), g.data_ptr(), u.data_ptr(),
+                                                     M * 8192, gpu.stream())),
+            12 * M * 8192)
+        a = t.randn(M * 2048, device=gpu.dev)
+        b = t.randn(M * 2048, device=gpu.dev)
+        rec(f"add M={M} n=2048",
+            lambda i: F.check(L.fgm_hip_add_dev(a.data_ptr(), b.data_ptr(), M * 2048, gpu.stream())),
+            12 * M * 2048)
+        q = t.randn(M, 8 * 256, device=gpu.dev)
+        inv = (1e6 ** (-np.arange(0, 256, 2, dtype=np.float64) / 256)).astype(np.float32)
+        cs = t.from_numpy(np.stack([kernels.rope_table(inv, 256, 100 + r) for r in range(M)])).to(gpu.dev)
+        rec(f"rope M={M} 8x256",
+            lambda i: F.check(L.fgm_hip_rope_dev(q.data_ptr(), M, 8, 256, cs.data_ptr(), gpu.stream())),
+            8 * M * 2048 + cs.numel() * 4)
+    lg = t.randn(8 * 262144, device=gpu.dev)
+    rec("softcap logits M=8 n=262144",
+        lambda i: F.check(L.fgm_hip_softcap_dev(lg.data_ptr(), 8 * 262144, 30.0, gpu.stream())),
+        8 * 8 * 262144)
+    return {"workload": "elementwise primitives, one launch each, graphs of 24 back-to-back "
+                        "launches (a launch costs >= 1.8 us on this box)", "per_op": res}
+
+
 # ------------------------------------------------------------ CPU baseline
 def cpu_baseline(host, budget_s=10.0):
     import numpy as np
@@ -485,7 +535,8 @@ def main():
     extra = {}
     if not args.no_extra:
         for name, fn in (("cfg1", extra_cfg1), ("int4_stream", extra_int4_stream),
-                         ("cfg3", extra_cfg3), ("cfg5", extra_cfg5), ("cfg4", extra_cfg4)):
+                         ("cfg3", extra_cfg3), ("cfg5", extra_cfg5), ("cfg4", extra_cfg4),
+                         ("elem", extra_elem)):
             log("extra", name)
             try:
                 extra[name] = fn(gpu)

@@ -66,11 +66,29 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_fwht_hip.argtypes = [p, i, i]
     L.fgm_hip_gemm_batch_dev.argtypes = [p, i, p]
     L.fgm_hip_prep_batch_dev.argtypes = [p, i, p]
+    L.fgm_rmsnorm_hip.argtypes = [p, p, p, i, f]
+    L.fgm_rmsnorm_noscale_hip.argtypes = [p, p, i, f]
+    L.fgm_gelu_mul_hip.argtypes = [p, p, p, i]
+    L.fgm_gelu_hip.argtypes = [p, i]
+    L.fgm_rope_hip.argtypes = [p, i, i, p, i]
+    L.fgm_add_hip.argtypes = [p, p, i]
+    L.fgm_mul_hip.argtypes = [p, p, i]
+    L.fgm_scale_hip.argtypes = [p, f, i]
+    L.fgm_softcap_hip.argtypes = [p, i, f]
+    L.fgm_hip_rmsnorm_dev.argtypes = [p, p, p, i, i, f, p]
+    L.fgm_hip_gelu_mul_dev.argtypes = [p, p, p, i, p]
+    L.fgm_hip_softcap_dev.argtypes = [p, i, f, p]
+    L.fgm_hip_rope_table.argtypes = [p, p, i, i]
+    L.fgm_hip_rope_dev.argtypes = [p, i, i, i, p, p]
+    L.fgm_hip_add_dev.argtypes = [p, p, i, p]
+    L.fgm_hip_mul_dev.argtypes = [p, p, i, p]
+    L.fgm_hip_scale_dev.argtypes = [p, f, i, p]
     for name in ("fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
-                 "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path"):
+                 "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path",
+                 "fgm_hip_rmsnorm_dev", "fgm_hip_gelu_mul_dev", "fgm_hip_softcap_dev",
+                 "fgm_hip_rope_dev", "fgm_hip_add_dev", "fgm_hip_mul_dev", "fgm_hip_scale_dev"):
         getattr(L, name).restype = i
-    del f
 
 
 def check(status: int) -> None:

@@ -17,6 +17,7 @@
 #include <mutex>
 #include <shared_mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/fgm_hip.h"
 #include "fgm_kernels.h"
@@ -576,5 +577,155 @@ static int dropin_fwht(float* x, int n, int hsz) {
 }
 
 void fgm_fwht_hip(float* x, int n, int hsz) { DROPIN(dropin_fwht(x, n, hsz), "fgm_fwht_hip"); }
+
+// ------------------------------------------------ elementwise, device API
+static int check_f32(const void* p, const char* name) {
+  return p ? FGM_HIP_OK : fail(FGM_HIP_EINVAL, "%s is NULL", name);
+}
+
+int fgm_hip_rmsnorm_dev(float* out, const float* x, const float* w, int rows, int n, float eps,
+                        void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (rows < 0 || n < 0) return fail(FGM_HIP_EINVAL, "rmsnorm: rows=%d n=%d", rows, n);
+  if (rows == 0 || n == 0) return FGM_HIP_OK;
+  if ((size_t)n * 4 > ROW_LDS_LIMIT) return fail(FGM_HIP_EINVAL, "rmsnorm: n=%d > 32768 (one row must fit in LDS)", n);
+  if ((rc = check_f32(out, "rmsnorm: out")) || (rc = check_f32(x, "rmsnorm: x"))) return rc;
+  hipError_t e = fgm_launch_rmsnorm(out, x, w, rows, n, eps, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "rmsnorm launch");
+}
+
+int fgm_hip_gelu_mul_dev(float* out, const float* gate, const float* up, int n, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (n <= 0) return n < 0 ? fail(FGM_HIP_EINVAL, "gelu_mul: n=%d", n) : FGM_HIP_OK;
+  if ((rc = check_f32(out, "gelu_mul: out")) || (rc = check_f32(gate, "gelu_mul: gate"))) return rc;
+  hipError_t e = fgm_launch_gelu(out, gate, up, n, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "gelu launch");
+}
+
+int fgm_hip_softcap_dev(float* x, int n, float cap, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (n <= 0) return n < 0 ? fail(FGM_HIP_EINVAL, "softcap: n=%d", n) : FGM_HIP_OK;
+  if ((rc = check_f32(x, "softcap: x"))) return rc;
+  hipError_t e = fgm_launch_softcap(x, n, cap, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "softcap launch");
+}
+
+void fgm_hip_rope_table(float* cs, const float* inv_freq, int head_dim, int pos) {
+  // ops.c:133-134, on the host with the host's libm
+  for (int j = 0; j < head_dim / 2; j++) {
+    const float a = (float)pos * inv_freq[j];
+    cs[2 * j] = cosf(a);
+    cs[2 * j + 1] = sinf(a);
+  }
+}
+
+int fgm_hip_rope_dev(float* x, int rows, int n_heads, int head_dim, const float* cs, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (rows < 0 || n_heads < 0 || head_dim < 0 || head_dim % 2)
+    return fail(FGM_HIP_EINVAL, "rope: rows=%d n_heads=%d head_dim=%d (even)", rows, n_heads, head_dim);
+  if (!rows || !n_heads || !head_dim) return FGM_HIP_OK;
+  if ((rc = check_f32(x, "rope: x")) || (rc = check_f32(cs, "rope: cs"))) return rc;
+  hipError_t e = fgm_launch_rope(x, rows, n_heads, head_dim, cs, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "rope launch");
+}
+
+static int binop_dev(float* a, const float* b, int n, int op, float s, void* stream, const char* what) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (n <= 0) return n < 0 ? fail(FGM_HIP_EINVAL, "%s: n=%d", what, n) : FGM_HIP_OK;
+  if ((rc = check_f32(a, what)) || (op < 2 && (rc = check_f32(b, what)))) return rc;
+  hipError_t e = fgm_launch_binop(a, b, n, op, s, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, what);
+}
+int fgm_hip_add_dev(float* a, const float* b, int n, void* stream) { return binop_dev(a, b, n, 0, 0.0f, stream, "add"); }
+int fgm_hip_mul_dev(float* a, const float* b, int n, void* stream) { return binop_dev(a, b, n, 1, 0.0f, stream, "mul"); }
+int fgm_hip_scale_dev(float* a, float s, int n, void* stream) { return binop_dev(a, nullptr, n, 2, s, stream, "scale"); }
+
+// ------------------------------------------------ elementwise, drop-ins
+// Host buffers through the per-thread staging buffers, synchronous, like the
+// reference's calls (lib.rs:47-59).
+static int up_f32(int slot, const float* h, int n, float** d) {
+  void* p;
+  int rc = staging(slot, (size_t)n * 4, &p);
+  if (rc) return rc;
+  *d = (float*)p;
+  if (h) HIPCHK(hipMemcpyAsync(p, h, (size_t)n * 4, hipMemcpyHostToDevice, g_stage.st));
+  return FGM_HIP_OK;
+}
+static int down_f32(float* h, const float* d, int n) {
+  HIPCHK(hipMemcpyAsync(h, d, (size_t)n * 4, hipMemcpyDeviceToHost, g_stage.st));
+  HIPCHK(hipStreamSynchronize(g_stage.st));
+  return FGM_HIP_OK;
+}
+
+static int dropin_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+  int rc = ensure_device();
+  if (rc || n <= 0) return rc;
+  float *dx, *dw = nullptr, *dout;
+  if ((rc = up_f32(0, x, n, &dx)) || (w && (rc = up_f32(1, w, n, &dw))) || (rc = up_f32(2, nullptr, n, &dout)))
+    return rc;
+  if ((rc = fgm_hip_rmsnorm_dev(dout, dx, dw, 1, n, eps, g_stage.st))) return rc;
+  return down_f32(out, dout, n);
+}
+void fgm_rmsnorm_hip(float* out, const float* x, const float* w, int n, float eps) {
+  DROPIN(dropin_rmsnorm(out, x, w, n, eps), "fgm_rmsnorm_hip");
+}
+void fgm_rmsnorm_noscale_hip(float* out, const float* x, int n, float eps) {
+  DROPIN(dropin_rmsnorm(out, x, nullptr, n, eps), "fgm_rmsnorm_noscale_hip");
+}
+
+static int dropin_gelu(float* out, const float* gate, const float* up, int n) {
+  int rc = ensure_device();
+  if (rc || n <= 0) return rc;
+  float *dg, *du = nullptr;
+  if ((rc = up_f32(0, gate, n, &dg)) || (up && (rc = up_f32(1, up, n, &du)))) return rc;
+  if ((rc = fgm_hip_gelu_mul_dev(dg, dg, du, n, g_stage.st))) return rc;
+  return down_f32(out, dg, n);
+}
+void fgm_gelu_mul_hip(float* out, const float* gate, const float* up, int n) {
+  DROPIN(dropin_gelu(out, gate, up, n), "fgm_gelu_mul_hip");
+}
+void fgm_gelu_hip(float* x, int n) { DROPIN(dropin_gelu(x, x, nullptr, n), "fgm_gelu_hip"); }
+
+static int dropin_rope(float* x, int n_heads, int head_dim, const float* inv_freq, int pos) {
+  int rc = ensure_device();
+  if (rc || n_heads <= 0 || head_dim <= 0) return rc;
+  const int n = n_heads * head_dim;
+  std::vector<float> cs((size_t)head_dim);
+  fgm_hip_rope_table(cs.data(), inv_freq, head_dim, pos);
+  float *dx, *dcs;
+  if ((rc = up_f32(0, x, n, &dx)) || (rc = up_f32(1, cs.data(), head_dim, &dcs))) return rc;
+  if ((rc = fgm_hip_rope_dev(dx, 1, n_heads, head_dim, dcs, g_stage.st))) return rc;
+  return down_f32(x, dx, n);
+}
+void fgm_rope_hip(float* x, int n_heads, int head_dim, const float* inv_freq, int pos) {
+  DROPIN(dropin_rope(x, n_heads, head_dim, inv_freq, pos), "fgm_rope_hip");
+}
+
+static int dropin_binop(float* a, const float* b, int n, int op, float s) {
+  int rc = ensure_device();
+  if (rc || n <= 0) return rc;
+  float *da, *db = nullptr;
+  if ((rc = up_f32(0, a, n, &da)) || (op < 2 && (rc = up_f32(1, b, n, &db)))) return rc;
+  if ((rc = binop_dev(da, db, n, op, s, g_stage.st, "binop"))) return rc;
+  return down_f32(a, da, n);
+}
+void fgm_add_hip(float* a, const float* b, int n) { DROPIN(dropin_binop(a, b, n, 0, 0.0f), "fgm_add_hip"); }
+void fgm_mul_hip(float* a, const float* b, int n) { DROPIN(dropin_binop(a, b, n, 1, 0.0f), "fgm_mul_hip"); }
+void fgm_scale_hip(float* a, float s, int n) { DROPIN(dropin_binop(a, nullptr, n, 2, s), "fgm_scale_hip"); }
+
+static int dropin_softcap(float* x, int n, float cap) {
+  int rc = ensure_device();
+  if (rc || n <= 0) return rc;
+  float* dx;
+  if ((rc = up_f32(0, x, n, &dx))) return rc;
+  if ((rc = fgm_hip_softcap_dev(dx, n, cap, g_stage.st))) return rc;
+  return down_f32(x, dx, n);
+}
+void fgm_softcap_hip(float* x, int n, float cap) { DROPIN(dropin_softcap(x, n, cap), "fgm_softcap_hip"); }
 
 }  // extern "C"

@@ -56,3 +56,14 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& b, hipStream_t st);
 
 // Dense MFMA path (any M).
 hipError_t fgm_launch_gemm(int bits, const GemmBatch& b, hipStream_t st);
+
+// f32 elementwise primitives (fgm_elem.hip).  rows x n contiguous rows for
+// rmsnorm (w NULL: no scale); gelu: up NULL for in-place gelu (out may be
+// gate); rope: cs [rows][head_dim / 2][2] (cos, sin); binop: 0 add, 1 mul,
+// 2 scale by s.
+hipError_t fgm_launch_rmsnorm(float* out, const float* x, const float* w, int rows, int n, float eps,
+                              hipStream_t st);
+hipError_t fgm_launch_gelu(float* out, const float* gate, const float* up, int n, hipStream_t st);
+hipError_t fgm_launch_softcap(float* x, int n, float cap, hipStream_t st);
+hipError_t fgm_launch_rope(float* x, int rows, int n_heads, int head_dim, const float* cs, hipStream_t st);
+hipError_t fgm_launch_binop(float* a, const float* b, int n, int op, float s, hipStream_t st);

@@ -216,3 +216,122 @@ def prep_batch(problems, stream=None) -> None:
 def gemm_path(bits: int, m: int, k: int, group: int = 64) -> str:
     """'skinny' or 'dense': which kernel family serves this shape."""
     return ("skinny", "dense")[lib().fgm_hip_gemm_path(bits, m, k, group)]
+
+
+# ------------------------------------------------------ elementwise ops
+# lib.rs:220-291.  Host (numpy) buffers go to the drop-ins, GPU tensors to the
+# device API on torch's current stream.
+def rmsnorm(out, x, w, eps: float) -> None:
+    """out = x * (mean(x^2) + eps)^-0.5 * w over n = len(w) (lib.rs:220-223)."""
+    n = _len(w)
+    assert _len(x) >= n and _len(out) >= n
+    backend()
+    if _kind(out, x, w) == "host":
+        lib().fgm_rmsnorm_hip(_hp(out), _hp(x), _hp(w), n, eps)
+    else:
+        check(lib().fgm_hip_rmsnorm_dev(_dp(out), _dp(x), _dp(w), 1, n, eps, _stream()))
+
+
+def rmsnorm_noscale(out, x, n: int, eps: float) -> None:
+    """rmsnorm without the learned scale (lib.rs:226-228)."""
+    assert _len(x) >= n and _len(out) >= n
+    backend()
+    if _kind(out, x) == "host":
+        lib().fgm_rmsnorm_noscale_hip(_hp(out), _hp(x), n, eps)
+    else:
+        check(lib().fgm_hip_rmsnorm_dev(_dp(out), _dp(x), None, 1, n, eps, _stream()))
+
+
+def rmsnorm_rows(out, x, w, rows: int, n: int, eps: float) -> None:
+    """Device API only: rmsnorm of `rows` contiguous rows (the forward pass
+    calls rmsnorm once per row or head, forward.rs:480-511)."""
+    backend()
+    if _kind(out, x, w) != "dev":
+        raise TypeError("rmsnorm_rows takes GPU tensors")
+    check(lib().fgm_hip_rmsnorm_dev(_dp(out), _dp(x), _ptr_or_none(w), rows, n, eps, _stream()))
+
+
+def gelu_mul(out, gate, up, n: int) -> None:
+    """out = gelu_tanh(gate) * up (lib.rs:231-233)."""
+    assert _len(gate) >= n and _len(up) >= n and _len(out) >= n
+    backend()
+    if _kind(out, gate, up) == "host":
+        lib().fgm_gelu_mul_hip(_hp(out), _hp(gate), _hp(up), n)
+    else:
+        check(lib().fgm_hip_gelu_mul_dev(_dp(out), _dp(gate), _dp(up), n, _stream()))
+
+
+def gelu(x) -> None:
+    """In-place gelu_tanh (lib.rs:236-239)."""
+    n = _len(x)
+    backend()
+    if _kind(x) == "host":
+        lib().fgm_gelu_hip(_hp(x), n)
+    else:
+        check(lib().fgm_hip_gelu_mul_dev(_dp(x), _dp(x), None, n, _stream()))
+
+
+def rope_table(inv_freq: np.ndarray, head_dim: int, pos: int) -> np.ndarray:
+    """(cos, sin) pairs for one position, computed on the host with the
+    host's libm exactly as ops.c:133-134 does: float32 [head_dim // 2, 2]."""
+    inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    cs = np.empty((head_dim // 2, 2), np.float32)
+    lib().fgm_hip_rope_table(cs.ctypes.data, inv.ctypes.data, head_dim, pos)
+    return cs
+
+
+def rope(x, n_heads: int, head_dim: int, inv_freq, pos: int) -> None:
+    """In-place half-split rotary embedding of one token's heads
+    (lib.rs:242-244).  On the device path inv_freq is a numpy array (host
+    side, where the angles are computed)."""
+    assert _len(x) >= n_heads * head_dim and head_dim % 2 == 0
+    backend()
+    if _kind(x) == "host":
+        inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+        lib().fgm_rope_hip(_hp(x), n_heads, head_dim, _hp(inv), pos)
+    else:
+        import torch
+        cs = torch.from_numpy(rope_table(inv_freq, head_dim, pos)).to(x.device)
+        check(lib().fgm_hip_rope_dev(_dp(x), 1, n_heads, head_dim, _dp(cs), _stream()))
+        x._fgm_keep = cs  # keep the table alive until the launch has run
+
+
+def add(a, b) -> None:
+    """a += b over min(len(a), len(b)) (lib.rs:270-273)."""
+    n = min(_len(a), _len(b))
+    backend()
+    if _kind(a, b) == "host":
+        lib().fgm_add_hip(_hp(a), _hp(b), n)
+    else:
+        check(lib().fgm_hip_add_dev(_dp(a), _dp(b), n, _stream()))
+
+
+def mul(a, b) -> None:
+    """a *= b (lib.rs:276-279)."""
+    n = min(_len(a), _len(b))
+    backend()
+    if _kind(a, b) == "host":
+        lib().fgm_mul_hip(_hp(a), _hp(b), n)
+    else:
+        check(lib().fgm_hip_mul_dev(_dp(a), _dp(b), n, _stream()))
+
+
+def scale(a, s: float) -> None:
+    """a *= s (lib.rs:282-285)."""
+    n = _len(a)
+    backend()
+    if _kind(a) == "host":
+        lib().fgm_scale_hip(_hp(a), s, n)
+    else:
+        check(lib().fgm_hip_scale_dev(_dp(a), s, n, _stream()))
+
+
+def softcap(x, cap: float) -> None:
+    """x = cap * tanh(x / cap) (lib.rs:288-291)."""
+    n = _len(x)
+    backend()
+    if _kind(x) == "host":
+        lib().fgm_softcap_hip(_hp(x), n, cap)
+    else:
+        check(lib().fgm_hip_softcap_dev(_dp(x), n, cap, _stream()))
+

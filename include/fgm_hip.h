@@ -126,6 +126,39 @@ int fgm_hip_quant_act_dev(const float *x, int rows, int k, int8_t *q, float *sca
 int fgm_hip_pack_a_dev(int m, int k, const int8_t *a, int8_t *ap, void *stream);
 int fgm_hip_fwht_dev(float *x, int n, int hsz, void *stream);
 
+/* ----------------------------------------------- elementwise primitives
+ * The forward pass's f32 operations that sit between the GEMMs (ops.c), so
+ * that activations stay on the GPU.  Results equal the reference's bytes
+ * (same operations in the same order), except the scalar tails of gelu and
+ * softcap when n % 16 != 0 (libm tanhf on the CPU, the device tanhf here;
+ * within a few ulp; no model dimension has such a tail). */
+
+/* drop-ins, host pointers, same parameters as the reference's symbols */
+void fgm_rmsnorm_hip(float *out, const float *x, const float *w, int n, float eps); /* lib.rs:47, ops.c:55-71 */
+void fgm_rmsnorm_noscale_hip(float *out, const float *x, int n, float eps);        /* lib.rs:48, ops.c:74-88 */
+void fgm_gelu_mul_hip(float *out, const float *gate, const float *up, int n);       /* lib.rs:49, ops.c:115-124 */
+void fgm_gelu_hip(float *x, int n);                                                 /* lib.rs:50, ops.c:106-112 */
+void fgm_rope_hip(float *x, int n_heads, int head_dim, const float *inv_freq, int pos); /* lib.rs:51, ops.c:130-142 */
+void fgm_add_hip(float *a, const float *b, int n);                                  /* lib.rs:56, ops.c:316-321 */
+void fgm_mul_hip(float *a, const float *b, int n);                                  /* lib.rs:57, ops.c:323-328 */
+void fgm_scale_hip(float *a, float s, int n);                                       /* lib.rs:58, ops.c:330-336 */
+void fgm_softcap_hip(float *x, int n, float cap);                                   /* lib.rs:59, ops.c:338-350 */
+
+/* device API: rmsnorm of `rows` contiguous rows of n floats each (w NULL:
+ * no scale, fgm_rmsnorm_noscale); gelu_mul with up NULL is gelu (out may be
+ * gate); rope on x [rows][n_heads][head_dim] with cs [rows][head_dim/2][2] =
+ * (cos, sin) pairs from fgm_hip_rope_table (host, the host's libm, as
+ * ops.c:133-134); add / mul / scale in place on a. */
+int fgm_hip_rmsnorm_dev(float *out, const float *x, const float *w, int rows, int n, float eps,
+                        void *stream);
+int fgm_hip_gelu_mul_dev(float *out, const float *gate, const float *up, int n, void *stream);
+int fgm_hip_softcap_dev(float *x, int n, float cap, void *stream);
+void fgm_hip_rope_table(float *cs, const float *inv_freq, int head_dim, int pos);
+int fgm_hip_rope_dev(float *x, int rows, int n_heads, int head_dim, const float *cs, void *stream);
+int fgm_hip_add_dev(float *a, const float *b, int n, void *stream);
+int fgm_hip_mul_dev(float *a, const float *b, int n, void *stream);
+int fgm_hip_scale_dev(float *a, float s, int n, void *stream);
+
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);

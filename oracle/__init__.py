@@ -74,6 +74,17 @@ def lib() -> C.CDLL:
         L.orc_gen_uniform.argtypes = [_u64, _sz, _f, _f, _p]
         L.orc_gen_normal.argtypes = [_u64, _sz, _p]
         L.orc_gen_student_t.argtypes = [_u64, _sz, _i, _p]
+        L.orc_exp16.restype = _f
+        L.orc_exp16.argtypes = [_f]
+        L.orc_rmsnorm.argtypes = [_p, _p, _p, _i, _f]
+        L.orc_rmsnorm_noscale.argtypes = [_p, _p, _i, _f]
+        L.orc_gelu_mul.argtypes = [_p, _p, _p, _i]
+        L.orc_gelu.argtypes = [_p, _i]
+        L.orc_rope.argtypes = [_p, _i, _i, _p, _i]
+        L.orc_add.argtypes = [_p, _p, _i]
+        L.orc_mul.argtypes = [_p, _p, _i]
+        L.orc_scale.argtypes = [_p, _f, _i]
+        L.orc_softcap.argtypes = [_p, _i, _f]
         L.orc_xorshift_fill.restype = _u64
         L.orc_xorshift_fill.argtypes = [_u64, _sz, _i, _i, _p]
         L.orc_lcg_fill.restype = C.c_uint32
@@ -97,6 +108,15 @@ def _bind_ref(L: C.CDLL) -> None:
     L.fgm_pack_a.argtypes = [_i, _i, _p, _p]
     L.fgm_fwht.argtypes = [_p, _i, _i]
     L.fgm_prep_rows.argtypes = [_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i]
+    L.fgm_rmsnorm.argtypes = [_p, _p, _p, _i, _f]
+    L.fgm_rmsnorm_noscale.argtypes = [_p, _p, _i, _f]
+    L.fgm_gelu_mul.argtypes = [_p, _p, _p, _i]
+    L.fgm_gelu.argtypes = [_p, _i]
+    L.fgm_rope.argtypes = [_p, _i, _i, _p, _i]
+    L.fgm_add.argtypes = [_p, _p, _i]
+    L.fgm_mul.argtypes = [_p, _p, _i]
+    L.fgm_scale.argtypes = [_p, _f, _i]
+    L.fgm_softcap.argtypes = [_p, _i, _f]
 
 
 def ref() -> C.CDLL | None:
@@ -300,3 +320,72 @@ def gemm_q4g(m, n, k, ap, a_scale, bq, b_scale, group, c, ldc, n0, n1) -> None:
     """fgm_gemm_q4g_vnni (vnni_gemm.c:291-322), in place on c."""
     lib().orc_gemm_q4g(m, n, k, _ptr(ap), _ptr(a_scale), _ptr(bq), _ptr(b_scale), group,
                        _ptr(c), ldc, n0, n1)
+
+
+# ------------------------------------------------------- elementwise ops
+# Restatements of ops.c's f32 primitives (fgm_oracle.c cites the lines).  All
+# take and return numpy float32 arrays; the in-place reference functions get
+# a copy.
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def exp16(x: float) -> float:
+    return lib().orc_exp16(x)
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray | None, eps: float) -> np.ndarray:
+    """One row (``fgm_rmsnorm``); ``w=None`` is ``fgm_rmsnorm_noscale``."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    if w is None:
+        lib().orc_rmsnorm_noscale(_ptr(out), _ptr(x), x.size, eps)
+    else:
+        w = _f32(w)
+        lib().orc_rmsnorm(_ptr(out), _ptr(x), _ptr(w), x.size, eps)
+    return out
+
+
+def gelu_mul(gate: np.ndarray, up: np.ndarray | None) -> np.ndarray:
+    """``fgm_gelu_mul`` (``up=None``: ``fgm_gelu``)."""
+    g = _f32(gate)
+    if up is None:
+        out = g.copy()
+        lib().orc_gelu(_ptr(out), out.size)
+        return out
+    u = _f32(up)
+    out = np.empty_like(g)
+    lib().orc_gelu_mul(_ptr(out), _ptr(g), _ptr(u), g.size)
+    return out
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, inv_freq: np.ndarray, pos: int) -> np.ndarray:
+    out = _f32(x).copy()
+    inv = _f32(inv_freq)
+    lib().orc_rope(_ptr(out), n_heads, head_dim, _ptr(inv), pos)
+    return out
+
+
+def add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = _f32(a).copy()
+    lib().orc_add(_ptr(out), _ptr(_f32(b)), out.size)
+    return out
+
+
+def mul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = _f32(a).copy()
+    lib().orc_mul(_ptr(out), _ptr(_f32(b)), out.size)
+    return out
+
+
+def scale(a: np.ndarray, s: float) -> np.ndarray:
+    out = _f32(a).copy()
+    lib().orc_scale(_ptr(out), s, out.size)
+    return out
+
+
+def softcap(x: np.ndarray, cap: float) -> np.ndarray:
+    out = _f32(x).copy()
+    lib().orc_softcap(_ptr(out), out.size, cap)
+    return out
+

@@ -430,3 +430,134 @@ void orc_gen_student_t(uint64_t seed, size_t n, int nu, float *out) {
     out[i] = (float)(z[0] / sqrt(chi / nu));
   }
 }
+
+/* ======================================================= elementwise ops
+ * The forward pass's f32 elementwise primitives, ops.c:17-38 (exp512_ps),
+ * :55-88 (rmsnorm), :90-124 (gelu), :126-142 (rope), :316-350 (add, mul,
+ * scale, softcap).  The reference processes 16 floats per AVX-512 vector and
+ * finishes with a scalar tail; both parts are restated element by element in
+ * the reference's operation order.  The reference is built by GCC, whose
+ * default for GNU C is -ffp-contract=fast: it fuses some scalar-tail
+ * expressions into one fma.  Where it does (determined against the compiled
+ * reference, tests/test_elem.py), this restatement writes fmaf explicitly. */
+
+/* exp512_ps (ops.c:20-38) on one lane: Cephes range reduction. */
+float orc_exp16(float x) {
+  x = fminf(fmaxf(x, -88.0f), 88.0f);
+  const float fx = rintf(x * 1.44269504088896341f); /* _mm512_roundscale_ps, RNE */
+  float z = fmaf(-fx, 0.693359375f, x);              /* _mm512_fnmadd_ps */
+  z = fmaf(-fx, -2.12194440e-4f, z);
+  float y = 1.9875691500E-4f;
+  y = fmaf(y, z, 1.3981999507E-3f);
+  y = fmaf(y, z, 8.3334519073E-3f);
+  y = fmaf(y, z, 4.1665795894E-2f);
+  y = fmaf(y, z, 1.6666665459E-1f);
+  y = fmaf(y, z, 5.0000001201E-1f);
+  y = fmaf(y, z * z, z);
+  y = y + 1.0f;
+  const int32_t n = (int32_t)fx; /* _mm512_cvtps_epi32 of an integral value */
+  const uint32_t bits = (uint32_t)(n + 127) << 23;
+  float p2;
+  memcpy(&p2, &bits, 4);
+  return y * p2;
+}
+
+/* _mm512_reduce_add_ps as GCC's avx512fintrin.h defines it: the upper eight
+ * lanes onto the lower eight, then four, then lanes {0,1} + {2,3}, then the
+ * last pair. */
+static float gcc_reduce_add16(const float *a) {
+  float t3[8], t6[4];
+  for (int j = 0; j < 8; j++) t3[j] = a[j + 8] + a[j];
+  for (int j = 0; j < 4; j++) t6[j] = t3[j + 4] + t3[j];
+  return (t6[0] + t6[2]) + (t6[1] + t6[3]);
+}
+
+/* sum of squares and 1/rms of one row (ops.c:58-66, 75-83): 16 lane
+ * accumulators, lane j takes x[16t + j] in ascending t by fma; GCC's tree;
+ * the tail fused as fmaf(x, x, ss); then 1 / sqrtf(ss / n + eps). */
+static float rms_inv(const float *x, int n, float eps) {
+  float acc[16] = {0};
+  int i = 0;
+  for (; i + 16 <= n; i += 16)
+    for (int j = 0; j < 16; j++) acc[j] = fmaf(x[i + j], x[i + j], acc[j]);
+  float ss = gcc_reduce_add16(acc);
+  for (; i < n; i++) ss = fmaf(x[i], x[i], ss);
+  return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+/* fgm_rmsnorm (ops.c:55-71): out = (x * inv) * w */
+void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
+  const float inv = rms_inv(x, n, eps);
+  for (int i = 0; i < n; i++) out[i] = (x[i] * inv) * w[i];
+}
+
+/* fgm_rmsnorm_noscale (ops.c:74-88): out = x * inv */
+void orc_rmsnorm_noscale(float *out, const float *x, int n, float eps) {
+  const float inv = rms_inv(x, n, eps);
+  for (int i = 0; i < n; i++) out[i] = x[i] * inv;
+}
+
+/* gelu_tanh_v (ops.c:93-104) on one lane */
+static float gelu_vec(float x) {
+  const float x3 = (x * x) * x;
+  const float u = 0.7978845608028654f * fmaf(0.044715f, x3, x);
+  const float e = orc_exp16(u + u);
+  const float t = 1.0f - 2.0f / (e + 1.0f);
+  return (0.5f * x) * (1.0f + t);
+}
+
+/* the scalar tail's gelu (ops.c:110, 120): libm tanhf; GCC fuses
+ * v + 0.044715f * v * v * v into fmaf((0.044715f * v) * v, v, v) */
+static float gelu_tail(float v) {
+  return (0.5f * v) * (1.0f + tanhf(0.7978845608028654f * fmaf((0.044715f * v) * v, v, v)));
+}
+
+/* fgm_gelu_mul (ops.c:115-124): out = gelu(gate) * up */
+void orc_gelu_mul(float *out, const float *gate, const float *up, int n) {
+  const int nv = n & ~15;
+  for (int i = 0; i < n; i++) out[i] = (i < nv ? gelu_vec(gate[i]) : gelu_tail(gate[i])) * up[i];
+}
+
+/* fgm_gelu (ops.c:106-112), in place */
+void orc_gelu(float *x, int n) {
+  const int nv = n & ~15;
+  for (int i = 0; i < n; i++) x[i] = i < nv ? gelu_vec(x[i]) : gelu_tail(x[i]);
+}
+
+/* fgm_rope (ops.c:130-142): a = pos * inv_freq[j], c = cosf(a), s = sinf(a)
+ * (libm); GCC fuses the rotation into fmaf(lo, c, -(hi * s)) and
+ * fmaf(hi, c, lo * s). */
+void orc_rope(float *x, int n_heads, int head_dim, const float *inv_freq, int pos) {
+  const int h = head_dim / 2;
+  for (int j = 0; j < h; j++) {
+    const float a = (float)pos * inv_freq[j];
+    const float c = cosf(a), s = sinf(a);
+    for (int hh = 0; hh < n_heads; hh++) {
+      float *p = x + (size_t)hh * head_dim;
+      const float lo = p[j], hi = p[j + h];
+      p[j] = fmaf(lo, c, -(hi * s));
+      p[j + h] = fmaf(hi, c, lo * s);
+    }
+  }
+}
+
+/* fgm_add / fgm_mul / fgm_scale (ops.c:316-336) */
+void orc_add(float *a, const float *b, int n) { for (int i = 0; i < n; i++) a[i] += b[i]; }
+void orc_mul(float *a, const float *b, int n) { for (int i = 0; i < n; i++) a[i] *= b[i]; }
+void orc_scale(float *a, float s, int n) { for (int i = 0; i < n; i++) a[i] *= s; }
+
+/* fgm_softcap (ops.c:338-350): vector part cap * (1 - 2 / (exp(2u) + 1)) with
+ * u = x * (1 / cap); tail cap * tanhf(x / cap) */
+void orc_softcap(float *x, int n, float cap) {
+  const float ci = 1.0f / cap;
+  const int nv = n & ~15;
+  for (int i = 0; i < n; i++) {
+    if (i < nv) {
+      const float u = x[i] * ci;
+      const float e = orc_exp16(u + u);
+      x[i] = cap * (1.0f - 2.0f / (e + 1.0f));
+    } else {
+      x[i] = cap * tanhf(x[i] / cap);
+    }
+  }
+}

@@ -155,3 +155,38 @@ def prep_input():
     src = oracle.gen_normal(21, m * lda).reshape(m, lda)
     src[3, 10] = 40.0
     return m, k, lda, src.astype(np.float32)
+
+
+# ---------------------------------------------------------- elementwise ops
+# Row lengths: model dimensions (hidden 2048 / 1536, intermediate 8192, head
+# 256 / 512) and ragged ones with a scalar tail (n % 16 != 0), as ops.c's
+# vector + tail structure has them.
+ELEM_NS = [16, 256, 512, 1536, 2048, 8192, 7, 31, 2063]
+
+
+def elem_inputs(n: int):
+    """Seeded inputs for one row length: x ~ 3 N(0,1), w and up ~ N(0,1),
+    gate ~ 2 N(0,1) (reaching exp's clamp region is the softcap input's job:
+    20 N(0,1) with cap 30)."""
+    x = oracle.gen_normal(0xE1E0 + n, n) * np.float32(3.0)
+    w = oracle.gen_normal(0xE1E1 + n, n)
+    up = oracle.gen_normal(0xE1E2 + n, n)
+    gate = oracle.gen_normal(0xE1E3 + n, n) * np.float32(2.0)
+    sc = oracle.gen_normal(0xE1E4 + n, n) * np.float32(20.0)
+    return dict(x=x.astype(np.float32), w=w, up=up, gate=gate.astype(np.float32),
+                sc=sc.astype(np.float32))
+
+
+# RoPE: a Gemma-style proportional table (theta 1e6, the last quarter of the
+# half-dimension zero: "nope" dims pass through, ops.c:127-129), 8 heads.
+ROPE_CASES = [(8, 256, 0), (8, 256, 1), (8, 256, 997), (4, 512, 32767), (2, 64, 5)]
+
+
+def rope_inputs(n_heads: int, head_dim: int):
+    h = head_dim // 2
+    j = np.arange(h, dtype=np.float64)
+    inv = (1.0e6 ** (-2.0 * j / head_dim)).astype(np.float32)
+    inv[3 * h // 4:] = 0.0
+    x = oracle.gen_normal(0xA0BE + head_dim, n_heads * head_dim)
+    return x, inv
+

@@ -141,6 +141,37 @@ def main() -> None:
                 "qs_bits": [int(v) for v in qs.view(np.uint32)]}
     out["prep_rows"] = prep
 
+    elem = {}
+    for n in cases.ELEM_NS:
+        e = cases.elem_inputs(n)
+        o1 = np.empty(n, np.float32)
+        R.fgm_rmsnorm(P(o1), P(e["x"]), P(e["w"]), n, 1e-6)
+        o2 = np.empty(n, np.float32)
+        R.fgm_rmsnorm_noscale(P(o2), P(e["x"]), n, 1e-6)
+        o3 = np.empty(n, np.float32)
+        R.fgm_gelu_mul(P(o3), P(e["gate"]), P(e["up"]), n)
+        o4 = e["gate"].copy()
+        R.fgm_gelu(P(o4), n)
+        o5 = e["sc"].copy()
+        R.fgm_softcap(P(o5), n, 30.0)
+        o6 = e["x"].copy()
+        R.fgm_add(P(o6), P(e["w"]), n)
+        o7 = e["x"].copy()
+        R.fgm_mul(P(o7), P(e["w"]), n)
+        o8 = e["x"].copy()
+        R.fgm_scale(P(o8), 0.7071067811865476, n)
+        elem[str(n)] = {name: digest(a) for name, a in (
+            ("rmsnorm", o1), ("rmsnorm_noscale", o2), ("gelu_mul", o3), ("gelu", o4),
+            ("softcap", o5), ("add", o6), ("mul", o7), ("scale", o8))}
+    rope = {}
+    for nh, hd, pos in cases.ROPE_CASES:
+        x, inv = cases.rope_inputs(nh, hd)
+        y = x.copy()
+        R.fgm_rope(P(y), nh, hd, P(inv), pos)
+        rope[f"{nh}x{hd}@{pos}"] = digest(y)
+    out["elem"] = elem
+    out["rope"] = rope
+
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_outputs.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
