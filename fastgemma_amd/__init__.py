@@ -83,7 +83,22 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_hip_add_dev.argtypes = [p, p, i, p]
     L.fgm_hip_mul_dev.argtypes = [p, p, i, p]
     L.fgm_hip_scale_dev.argtypes = [p, f, i, p]
-    for name in ("fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
+    L.fgm_attend_q8_hip.argtypes = [p, p, p, p, p, p, i, i, i, i, i, p]
+    L.fgm_attend_q8_heads_hip.argtypes = [p, p, p, p, p, p, i, i, i, i, i, p, i, i, i, i]
+    L.fgm_attend_q8_row_hip.argtypes = [p, p, p, p, p, p, i, i, i, i, i, p, i, i]
+    L.fgm_store_v_t_hip.argtypes = [p, p, i, i]
+    L.fgm_set_scalar_wfill_hip.argtypes = [i]
+    L.fgm_rowbatch_scratch_hip.argtypes = [i, i, i]
+    L.fgm_rowbatch_scratch_hip.restype = i
+    L.fgm_hip_attend_scratch_bytes.argtypes = [i, i, i, i, i]
+    L.fgm_hip_attend_scratch_bytes.restype = _C.c_size_t
+    L.fgm_hip_attend_dev.argtypes = [p, p, p, i, i, i, i, i, p, _C.c_size_t, p]
+    L.fgm_hip_attend_heads_dev.argtypes = [p, p, p, p, p, p, i, i, i, i, i, i, i, i, i, p,
+                                           _C.c_size_t, p]
+    L.fgm_hip_store_v_t_dev.argtypes = [p, p, i, i, p]
+    L.fgm_hip_kv_store_dev.argtypes = [p, p, i, i, p, p, p, p, i, i, i, p]
+    for name in ("fgm_hip_attend_dev", "fgm_hip_attend_heads_dev", "fgm_hip_store_v_t_dev",
+                 "fgm_hip_kv_store_dev", "fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
                  "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path",
                  "fgm_hip_rmsnorm_dev", "fgm_hip_gelu_mul_dev", "fgm_hip_softcap_dev",
@@ -111,6 +126,13 @@ class PrepDesc(_C.Structure):
                 ("qa", _C.c_void_p), ("qs", _C.c_void_p), ("pa", _C.c_void_p),
                 ("m", _C.c_int), ("k", _C.c_int), ("hsz", _C.c_int), ("r0", _C.c_int),
                 ("r1", _C.c_int)]
+
+
+class AttnSeq(_C.Structure):
+    """fgm_hip_attn_seq (include/fgm_hip.h)."""
+    _fields_ = [("kc", _C.c_void_p), ("ks", _C.c_void_p), ("vc", _C.c_void_p),
+                ("vs", _C.c_void_p), ("k_len", _C.c_int), ("ring", _C.c_int), ("pos", _C.c_int),
+                ("rows", _C.c_int)]
 
 
 from .kernels import (  # noqa: E402,F401

@@ -241,8 +241,8 @@ int cached_upload(const void* host, size_t bytes, void** dev) {
 // while the HIP runtime is being torn down at exit is not safe).
 struct Staging {
   hipStream_t st = nullptr;
-  void* buf[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-  size_t cap[6] = {0, 0, 0, 0, 0, 0};
+  void* buf[8] = {};
+  size_t cap[8] = {};
 };
 thread_local Staging g_stage;
 
@@ -728,4 +728,240 @@ static int dropin_softcap(float* x, int n, float cap) {
 }
 void fgm_softcap_hip(float* x, int n, float cap) { DROPIN(dropin_softcap(x, n, cap), "fgm_softcap_hip"); }
 
+// ------------------------------------------------------ int8-KV attention
+// Validates the sequences, fills the row bookkeeping and the grid of `a`
+// (scratch pointers excepted); *max_n, *max_span receive the longest range
+// and the longest range-or-ring of any row.
+static int attn_plan(AttnArgs& a, int* max_n, int* max_span) {
+  if (a.nh <= 0 || a.kvh <= 0 || a.nh % a.kvh)
+    return fail(FGM_HIP_EINVAL, "attend: n_heads=%d is not a multiple of kv_heads=%d", a.nh, a.kvh);
+  if (a.nh / a.kvh > 16) return fail(FGM_HIP_EINVAL, "attend: %d query heads per kv head > 16", a.nh / a.kvh);
+  if (a.hd < 64 || a.hd > 512 || a.hd % 64)
+    return fail(FGM_HIP_EINVAL, "attend: head_dim=%d must be a multiple of 64 in [64, 512]", a.hd);
+  if (a.h0 < 0 || a.h1 > a.nh || a.h0 > a.h1)
+    return fail(FGM_HIP_EINVAL, "attend: head range [%d,%d) outside [0,%d)", a.h0, a.h1, a.nh);
+  if (a.window < 0) return fail(FGM_HIP_EINVAL, "attend: window=%d", a.window);
+  if (a.nseq < 0 || a.nseq > FGM_ATTN_MAX_SEQ)
+    return fail(FGM_HIP_EINVAL, "attend: %d sequences (at most %d per call)", a.nseq, FGM_ATTN_MAX_SEQ);
+  if (!a.out || !a.q) return fail(FGM_HIP_EINVAL, "attend: out or q is NULL");
+  int m = 0, mn = 0, ms = 1, p1max = 1, p3max = 1;
+  long long tiles = 0;
+  for (int i = 0; i < a.nseq; i++) {
+    AttnSeq& s = a.seq[i];
+    if (s.nrows < 0) return fail(FGM_HIP_EINVAL, "attend: sequence %d has %d rows", i, s.nrows);
+    if (s.nrows && (!s.kc || !s.ks || !s.vc || !s.vs))
+      return fail(FGM_HIP_EINVAL, "attend: sequence %d has a NULL cache pointer", i);
+    if (s.k_len <= 0 || s.ring < 0 || s.ring > s.k_len)
+      return fail(FGM_HIP_EINVAL, "attend: sequence %d: k_len=%d ring=%d", i, s.k_len, s.ring);
+    s.row0 = m;
+    m += s.nrows;
+    for (int j = 0; j < s.nrows; j++) {
+      const AttnSpan sp = attn_span(s.pos0 + j + 1, s.lo, a.window, s.ring);
+      if (sp.st < 0 || sp.n < 0)
+        return fail(FGM_HIP_EINVAL, "attend: sequence %d row %d: range [%d,%d)", i, j, sp.st, sp.en);
+      if (!s.ring && sp.en > s.k_len)
+        return fail(FGM_HIP_EINVAL, "attend: sequence %d row %d: position %d outside a cache of %d",
+                    i, j, sp.en - 1, s.k_len);
+      if (s.ring && sp.n > s.ring)
+        return fail(FGM_HIP_EINVAL, "attend: sequence %d row %d: %d positions exceed the ring of %d",
+                    i, j, sp.n, s.ring);
+      if (sp.n > FGM_ATTN_MAX_SPAN)
+        return fail(FGM_HIP_EINVAL, "attend: %d positions in one row (at most %d)", sp.n, FGM_ATTN_MAX_SPAN);
+      mn = std::max(mn, sp.n);
+      ms = std::max(ms, std::max(sp.n, s.ring));
+      tiles += (sp.n + 15) / 16;
+      p3max = std::max(p3max, std::max(1, (sp.dom_steps + 3) / 4));
+    }
+  }
+  // positions per score workgroup: one 16-position tile per wave while the
+  // launch is small, more once it has thousands of tiles
+  const int tpw = (int)std::min<long long>(16, std::max<long long>(1, tiles / (4 * 2048)));
+  a.p1_chunk = 64 * tpw;
+  p1max = std::max(1, (mn + a.p1_chunk - 1) / a.p1_chunk);
+  a.m = m;
+  a.p1_chunks = p1max;
+  a.p3_chunks = p3max;
+  *max_n = mn;
+  *max_span = ms;
+  return FGM_HIP_OK;
+}
+
+static int attn_run(AttnArgs& a, void* scratch, size_t scratch_bytes, hipStream_t st) {
+  int max_n, max_span, rc;
+  if ((rc = attn_plan(a, &max_n, &max_span))) return rc;
+  if (a.m == 0 || a.h0 == a.h1) return FGM_HIP_OK;
+  const size_t need = fgm_attn_layout(nullptr, nullptr, a.m, a.nh, a.kvh, a.hd, max_span);
+  if (!scratch || scratch_bytes < need)
+    return fail(FGM_HIP_EINVAL, "attend: scratch of %zu bytes, this call needs %zu", scratch_bytes, need);
+  if (((uintptr_t)scratch) & 255) return fail(FGM_HIP_EINVAL, "attend: scratch must be 256-byte aligned");
+  fgm_attn_layout(&a, scratch, a.m, a.nh, a.kvh, a.hd, max_span);
+  hipError_t e = fgm_launch_attn(a, max_n, st);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "attention launch");
+}
+
+size_t fgm_hip_attend_scratch_bytes(int m, int n_heads, int kv_heads, int head_dim, int max_span) {
+  if (m <= 0 || n_heads <= 0 || kv_heads <= 0 || n_heads % kv_heads || head_dim <= 0) return 0;
+  return fgm_attn_layout(nullptr, nullptr, m, n_heads, kv_heads, head_dim, std::max(max_span, 1));
+}
+
+int fgm_hip_attend_dev(float* out, const float* q, const fgm_hip_attn_seq* seqs, int nseq,
+                       int n_heads, int kv_heads, int head_dim, int window, void* scratch,
+                       size_t scratch_bytes, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (nseq < 0 || nseq > FGM_ATTN_MAX_SEQ || (nseq && !seqs))
+    return fail(FGM_HIP_EINVAL, "attend: bad sequence array (count %d, at most %d)", nseq, FGM_ATTN_MAX_SEQ);
+  AttnArgs a{};
+  for (int i = 0; i < nseq; i++) {
+    const fgm_hip_attn_seq& s = seqs[i];
+    a.seq[i] = AttnSeq{s.kc, s.ks, s.vc, s.vs, s.k_len, s.ring, s.pos, 0, s.rows, 0};
+  }
+  a.nseq = nseq, a.nh = n_heads, a.kvh = kv_heads, a.hd = head_dim, a.window = window;
+  a.h0 = 0, a.h1 = n_heads, a.out = out, a.q = q;
+  return attn_run(a, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+int fgm_hip_attend_heads_dev(float* out, const float* q, const int8_t* kc, const float* ks,
+                             const int8_t* vc, const float* vs, int n_heads, int kv_heads,
+                             int head_dim, int start, int end, int h0, int h1, int ring, int cap,
+                             void* scratch, size_t scratch_bytes, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (start < 0 || end < start)
+    return fail(FGM_HIP_EINVAL, "attend_heads: range [%d,%d)", start, end);
+  AttnArgs a{};
+  a.seq[0] = AttnSeq{kc, ks, vc, vs, cap, ring, end - 1, start, 1, 0};
+  a.nseq = 1, a.nh = n_heads, a.kvh = kv_heads, a.hd = head_dim, a.window = 0;
+  a.h0 = h0, a.h1 = h1, a.out = out, a.q = q;
+  return attn_run(a, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+int fgm_hip_store_v_t_dev(int8_t* vt, const int8_t* src, int n, int slot, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (n < 0 || slot < 0) return fail(FGM_HIP_EINVAL, "store_v_t: n=%d slot=%d", n, slot);
+  if (n && (!vt || !src)) return fail(FGM_HIP_EINVAL, "store_v_t: NULL buffer");
+  hipError_t e = fgm_launch_store_v_t(vt, src, n, slot, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "store_v_t launch");
+}
+
+int fgm_hip_kv_store_dev(const float* k, const float* v, int m, int row_len, int8_t* kc, float* ks,
+                         int8_t* vt, float* vs, int cap, int pos, int ring, void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (m < 0 || row_len < 0 || pos < 0 || ring < 0 || cap < 0)
+    return fail(FGM_HIP_EINVAL, "kv_store: m=%d row_len=%d cap=%d pos=%d ring=%d", m, row_len, cap, pos, ring);
+  if (ring ? ring > cap : (long long)pos + m > cap)
+    return fail(FGM_HIP_EINVAL, "kv_store: positions [%d,%d) do not fit a cache of %d slots (ring %d)", pos,
+                pos + m, cap, ring);
+  if (row_len > 8192) return fail(FGM_HIP_EINVAL, "kv_store: row_len=%d > 8192", row_len);
+  if (ring && m > ring) return fail(FGM_HIP_EINVAL, "kv_store: %d rows overwrite each other in a ring of %d", m, ring);
+  if (m && (!k || !v || !kc || !ks || !vt || !vs)) return fail(FGM_HIP_EINVAL, "kv_store: NULL buffer");
+  hipError_t e = fgm_launch_kv_store(k, v, m, row_len, kc, ks, vt, vs, pos, ring, (hipStream_t)stream);
+  return e == hipSuccess ? FGM_HIP_OK : hip_fail(e, "kv_store launch");
+}
+
+// drop-ins: the caches move to the device per call (they are the caller's
+// mutable host buffers); `scratch` is the reference's host scratch and is
+// not touched.
+static int dropin_attend(float* out, const float* q, const int8_t* kc, const float* ks,
+                         const int8_t* vc, const float* vs, int n_heads, int kv_heads, int head_dim,
+                         int start, int end, int h0, int h1, int ring, int cap) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (n_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || cap <= 0 || h1 <= h0) {
+    AttnArgs a{};
+    a.nh = n_heads, a.kvh = kv_heads, a.hd = head_dim, a.h0 = h0, a.h1 = h1;
+    int mn, ms;
+    a.out = out, a.q = q;
+    return attn_plan(a, &mn, &ms);  // reports the invalid argument, or nothing to do
+  }
+  const size_t kvd = (size_t)kv_heads * head_dim;
+  const size_t kb = (size_t)cap * kvd, vb = (size_t)(cap + 3) / 4 * 4 * kvd, ob = (size_t)n_heads * head_dim * 4;
+  const int span = std::max(std::max(end - start, ring), 1);
+  const size_t sb = fgm_hip_attend_scratch_bytes(1, n_heads, kv_heads, head_dim, span);
+  void *dq, *dkc, *dks, *dvc, *dvs, *dout, *dsc;
+  if ((rc = staging(0, ob, &dq)) || (rc = staging(1, kb, &dkc)) || (rc = staging(2, (size_t)cap * 4, &dks)) ||
+      (rc = staging(3, vb, &dvc)) || (rc = staging(4, (size_t)cap * 4, &dvs)) || (rc = staging(5, ob, &dout)) ||
+      (rc = staging(6, sb, &dsc)))
+    return rc;
+  hipStream_t st = g_stage.st;
+  HIPCHK(hipMemcpyAsync(dq, q, ob, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(dkc, kc, kb, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(dks, ks, (size_t)cap * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(dvc, vc, vb, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(dvs, vs, (size_t)cap * 4, hipMemcpyHostToDevice, st));
+  if ((rc = fgm_hip_attend_heads_dev((float*)dout, (const float*)dq, (const int8_t*)dkc, (const float*)dks,
+                                     (const int8_t*)dvc, (const float*)dvs, n_heads, kv_heads, head_dim,
+                                     start, end, h0, h1, ring, cap, dsc, sb, st)))
+    return rc;
+  const size_t o0 = (size_t)h0 * head_dim, on = (size_t)(h1 - h0) * head_dim;
+  HIPCHK(hipMemcpyAsync(out + o0, (float*)dout + o0, on * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  return FGM_HIP_OK;
+}
+
+void fgm_attend_q8_heads_hip(float* out, const float* q, const int8_t* kc, const float* ks,
+                             const int8_t* vc, const float* vs, int n_heads, int kv_heads,
+                             int head_dim, int start, int end, float* scratch, int h0, int h1,
+                             int ring, int cap) {
+  (void)scratch;
+  // an empty or reversed range gives zeros, as the reference's loops do
+  DROPIN(dropin_attend(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start, std::max(end, start),
+                       h0, h1, ring, cap),
+         "fgm_attend_q8_heads_hip");
+}
+
+void fgm_attend_q8_hip(float* out, const float* q, const int8_t* kc, const float* ks, const int8_t* vc,
+                       const float* vs, int n_heads, int kv_heads, int head_dim, int start, int end,
+                       float* scratch) {
+  (void)scratch;
+  DROPIN(dropin_attend(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start, std::max(end, start), 0,
+                       n_heads, 0, std::max(end, 1)),
+         "fgm_attend_q8_hip");
+}
+
+void fgm_attend_q8_row_hip(float* out, const float* q, const int8_t* kc, const float* ks,
+                           const int8_t* vc, const float* vs, int n_heads, int kv_heads, int head_dim,
+                           int start, int end, float* scratch, int ring, int cap) {
+  (void)scratch;
+  // ops.c:734-744: an empty range zeroes every head (the device path gives
+  // zeros for an empty range); kv_heads != 1 takes the per-head path; the
+  // head-batched path computes at most eight heads (ops.c:749)
+  const int h1 = (end - start <= 0 || kv_heads != 1) ? n_heads : std::min(n_heads, 8);
+  DROPIN(dropin_attend(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start,
+                       std::max(end, start), 0, h1, ring, cap),
+         "fgm_attend_q8_row_hip");
+}
+
+static int dropin_store_v_t(int8_t* vt, const int8_t* src, int n, int slot) {
+  int rc = ensure_device();
+  if (rc || n <= 0) return rc;
+  if (slot < 0) return fail(FGM_HIP_EINVAL, "store_v_t: slot=%d", slot);
+  // the n * 4 bytes of slot's four-slot group
+  int8_t* grp = vt + (size_t)(slot >> 2) * n * 4;
+  void *dg, *ds;
+  if ((rc = staging(0, (size_t)n * 4, &dg)) || (rc = staging(1, (size_t)n, &ds))) return rc;
+  hipStream_t st = g_stage.st;
+  HIPCHK(hipMemcpyAsync(dg, grp, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(hipMemcpyAsync(ds, src, (size_t)n, hipMemcpyHostToDevice, st));
+  if ((rc = fgm_hip_store_v_t_dev((int8_t*)dg, (const int8_t*)ds, n, slot & 3, st))) return rc;
+  HIPCHK(hipMemcpyAsync(grp, dg, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  return FGM_HIP_OK;
+}
+
+void fgm_store_v_t_hip(int8_t* vt, const int8_t* src, int n, int slot) {
+  DROPIN(dropin_store_v_t(vt, src, n, slot), "fgm_store_v_t_hip");
+}
+
+// The reference keeps this flag for an A/B switch that its kernels no longer
+// read (ops.c:53-54); accepted and ignored.
+void fgm_set_scalar_wfill_hip(int on) { (void)on; }
+
+int fgm_rowbatch_scratch_hip(int n_heads, int cap, int head_dim) {
+  return n_heads * cap + (cap + 3) / 2 + 2 * head_dim + 64;
+}
+
 }  // extern "C"
+

@@ -1,0 +1,527 @@
+// fgm_attn.hip -- int8-KV attention on gfx950: fgm_attend_q8_heads /
+// fgm_attend_q8_row (ops.c:353-877), the transposed V store (ops.c:653-657)
+// and the forward pass's KV append (forward.rs:515-548).
+//
+// One call is three launches:
+//  1. attn_scores_kernel: s = ((float)(K.q) * qscale) * kscale for every
+//     (row, head, position).  Each workgroup makes the per-head int8 query
+//     (amax, 127 / amax, round to nearest even, clamp +-127; ops.c:417-433);
+//     K.q is an exact int32 on v_mfma_i32_16x16x64_i8 (heads x positions),
+//     equal to the reference's biased vpdpbusd sum minus its correction.
+//  2. attn_softmax_kernel, one workgroup per (row, head): the maximum, the
+//     exponentials (exp512_ps restated for the 16-wide chunks, a correctly
+//     rounded exp for the n % 16 tail), the reference's summation order (16
+//     lane sums in chunk order, GCC's reduce tree, the tail in order), then
+//     the 16-bit weights iw = (int)fma((e * inv) * vs, 65535 / wmax, 0.5)
+//     clamped to [0, 65535], written by slot as three 7-bit planes
+//     (iw = a 2^14 + b 2^7 + c).  A slot's weight is multiplied by the number
+//     of the reference's four-slot-aligned run spans that contain it, since
+//     ops.c:605-631 walks each span in turn.
+//  3. attn_pv_kernel: out = (float)(sum over slots of iw v) * (wmax / 65535):
+//     the planes against the transposed V cache on v_mfma_i32_16x16x64_i8,
+//     exact int32 partial sums added with device atomics (integer addition is
+//     order-free), and the last workgroup of a (row, kv head) converts.
+// Everything that is not integer arithmetic follows the reference's
+// operation order, so outputs equal its bytes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "fgm_common.h"
+#include "fgm_kernels.h"
+
+namespace {
+
+// exp512_ps (ops.c:20-38) on one lane
+FGM_DEV float exp16(float x) {
+  x = __builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f);
+  const float fx = __builtin_rintf(x * 1.44269504088896341f);
+  float z = __builtin_fmaf(-fx, 0.693359375f, x);
+  z = __builtin_fmaf(-fx, -2.12194440e-4f, z);
+  float y = 1.9875691500E-4f;
+  y = __builtin_fmaf(y, z, 1.3981999507E-3f);
+  y = __builtin_fmaf(y, z, 8.3334519073E-3f);
+  y = __builtin_fmaf(y, z, 4.1665795894E-2f);
+  y = __builtin_fmaf(y, z, 1.6666665459E-1f);
+  y = __builtin_fmaf(y, z, 5.0000001201E-1f);
+  y = __builtin_fmaf(y, z * z, z);
+  y = y + 1.0f;
+  return y * __int_as_float(((int)fx + 127) << 23);
+}
+
+template <int R>
+FGM_DEV float row_ror(float v) {  // lane j of a 16-lane row reads lane (j + R) % 16
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+
+FGM_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// max over the workgroup; `red` holds one float per wave; every thread gets it
+FGM_DEV float block_max(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+  for (int i = 1; i < nw; i++) m = __builtin_fmaxf(m, red[i]);
+  return m;
+}
+
+// One row's view of its sequence: cache, attended range and slot runs.
+struct Geo {
+  const int8_t* kc;
+  const float* ks;
+  const int8_t* vc;
+  const float* vs;
+  int k_len, ring, st, en, n;
+  int nrun, lo0, hi0, lo1, hi1;
+  int dom_lo, dom_steps;  // slot domain of the P.V kernel: [dom_lo, dom_lo + 64 dom_steps)
+};
+
+FGM_DEV Geo row_geo(const AttnArgs& a, int r) {
+  // the sequence holding row r, selected field by field (no dynamic index
+  // into the kernel argument)
+  const int8_t* kc = a.seq[0].kc;
+  const float* ks = a.seq[0].ks;
+  const int8_t* vc = a.seq[0].vc;
+  const float* vs = a.seq[0].vs;
+  int k_len = a.seq[0].k_len, ring = a.seq[0].ring, pos0 = a.seq[0].pos0, lo = a.seq[0].lo,
+      row0 = a.seq[0].row0;
+#pragma unroll
+  for (int j = 1; j < FGM_ATTN_MAX_SEQ; j++) {
+    if (j < a.nseq && r >= a.seq[j].row0) {
+      kc = a.seq[j].kc, ks = a.seq[j].ks, vc = a.seq[j].vc, vs = a.seq[j].vs;
+      k_len = a.seq[j].k_len, ring = a.seq[j].ring, pos0 = a.seq[j].pos0, lo = a.seq[j].lo;
+      row0 = a.seq[j].row0;
+    }
+  }
+  const AttnSpan sp = attn_span(pos0 + (r - row0) + 1, lo, a.window, ring);
+  Geo g;
+  g.kc = kc, g.ks = ks, g.vc = vc, g.vs = vs, g.k_len = k_len, g.ring = ring;
+  g.st = sp.st, g.en = sp.en, g.n = sp.n, g.nrun = sp.nrun;
+  g.lo0 = sp.lo0, g.hi0 = sp.hi0, g.lo1 = sp.lo1, g.hi1 = sp.hi1;
+  g.dom_lo = sp.dom_lo, g.dom_steps = sp.dom_steps;
+  return g;
+}
+
+// ------------------------------------------------------------- 1. scores
+// grid (p1_chunks, m * kvh), 256 threads; wave w takes the 16-position tiles
+// w, w + 4, ... of the workgroup's chunk.
+template <int KS>  // head_dim / 64
+__global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
+  constexpr int HD = KS * 64, QROW = HD + 16;  // padded LDS row: conflict-free fragment reads
+  __shared__ __attribute__((aligned(16))) int8_t qq[16 * QROW];
+  __shared__ float qsc[16];
+  const int r = blockIdx.y / a.kvh, g = blockIdx.y - r * a.kvh;
+  const Geo G = row_geo(a, r);
+  const int t_beg = G.st + (int)blockIdx.x * a.p1_chunk;
+  if (t_beg >= G.en) return;
+  const int grp = a.nh / a.kvh;
+  const int hb = max(a.h0, g * grp), he = min(a.h1, (g + 1) * grp);
+  if (hb >= he) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  // per-head int8 query, one wave per head row; rows past the group are zero
+  for (int hl = w; hl < 16; hl += 4) {
+    const int h = g * grp + hl;
+    const bool live = hl < grp && h >= hb && h < he;
+    float x[KS];
+    float amax = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      x[kk] = live ? a.q[((size_t)r * a.nh + h) * HD + 64 * kk + lane] : 0.0f;
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(x[kk]));
+    }
+    amax = wave_max(amax);
+    const float qinv = amax > 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      const float v = __builtin_amdgcn_fmed3f(__builtin_rintf(x[kk] * qinv), -127.0f, 127.0f);
+      qq[hl * QROW + 64 * kk + lane] = (int8_t)(int)v;
+    }
+    if (lane == 0) qsc[hl] = amax / 127.0f;
+  }
+  __syncthreads();
+
+  // A: lane row lane % 16 (head), bytes 16 (lane / 16) .. of each 64-dim step
+  v4i A[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; kk++)
+    A[kk] = *(const v4i*)(qq + (lane & 15) * QROW + 64 * kk + 16 * (lane >> 4));
+  const int kvd = a.kvh * HD;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(G.kc, (uint32_t)((size_t)G.k_len * kvd));
+  const int t_end = min(t_beg + a.p1_chunk, G.en);
+  float* srow = a.sc + (size_t)r * a.nh * a.sc_stride;
+  for (int t0 = t_beg + 16 * w; t0 < t_end; t0 += 64) {
+    const int t = t0 + (lane & 15);
+    const bool ok = t < t_end;
+    const int slot = G.ring ? t % G.ring : t;
+    const uint32_t base = ok ? (uint32_t)slot * (uint32_t)kvd + (uint32_t)(g * HD + 16 * (lane >> 4)) : FGM_OOB;
+    v4i B[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) B[kk] = buf_load_b128(rk, base, 64 * kk);
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) acc = mfma16(A[kk], B[kk], acc);
+    // D: lane, register i -> head row 4 (lane / 16) + i, position t
+    if (ok) {
+      const float kscale = G.ks[slot];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int hl = 4 * (lane >> 4) + i, h = g * grp + hl;
+        if (hl < grp && h >= hb && h < he)
+          srow[(size_t)h * a.sc_stride + (t - G.st)] = ((float)acc[i] * qsc[hl]) * kscale;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------- 2. softmax, weights
+// grid (m * (h1 - h0)), T threads; dynamic LDS: the exponentials transposed,
+// e[16 c + j] at lds[j * S + c] (S = 4 mod 64, >= n / 16 + 16), then the
+// reduction slots.
+FGM_DEV int exp_stride(int n) { return (((n + 15) >> 4) + 16 + 63) / 64 * 64 + 4; }
+
+__global__ __launch_bounds__(1024) void attn_softmax_kernel(const AttnArgs a) {
+  extern __shared__ float lds[];
+  const int nhr = a.h1 - a.h0;
+  const int r = blockIdx.x / nhr, h = a.h0 + ((int)blockIdx.x - r * nhr);
+  const int grp = a.nh / a.kvh, g = h / grp, hl = h - g * grp;
+  const Geo G = row_geo(a, r);
+  const int tid = threadIdx.x, T = blockDim.x, nw = T >> 6;
+  const int n = max(G.n, 0), n16 = n & ~15;
+  const int S = exp_stride(n);
+  float* red = lds + 16 * S;
+  const float* scr = a.sc + ((size_t)r * a.nh + h) * a.sc_stride;
+
+  float mx = -INFINITY;
+  for (int u = tid; u < n; u += T) mx = __builtin_fmaxf(mx, scr[u]);
+  mx = block_max(mx, red);
+  for (int u = tid; u < n; u += T) {
+    const float x = scr[u] - mx;
+    lds[(u & 15) * S + (u >> 4)] = u < n16 ? exp16(x) : (float)exp((double)x);
+  }
+  __syncthreads();
+  if (tid < 16) {
+    // lane j: e[16 c + j] summed in chunk order, reads two groups ahead
+    const int nt = n16 >> 4;
+    const float* c = lds + tid * S;
+    float acc = 0.0f;
+    float4 P[4], Q[4];
+    auto rd = [&](float4* p, int t0) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) p[q] = *(const float4*)(c + t0 + 4 * q);
+    };
+    auto add = [&](const float4* p) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        acc = acc + p[q].x;
+        acc = acc + p[q].y;
+        acc = acc + p[q].z;
+        acc = acc + p[q].w;
+      }
+    };
+    int t = 0;
+    rd(P, 0);
+    for (; t + 32 <= nt; t += 32) {
+      rd(Q, t + 16);
+      __builtin_amdgcn_sched_barrier(0);
+      add(P);
+      __builtin_amdgcn_sched_barrier(0);
+      rd(P, t + 32);
+      __builtin_amdgcn_sched_barrier(0);
+      add(Q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t + 16 <= nt) {
+      add(P);
+      t += 16;
+    }
+    for (; t < nt; t++) acc = acc + c[t];
+    // _mm512_reduce_add_ps
+    acc = acc + row_ror<8>(acc);
+    acc = acc + row_ror<4>(acc);
+    acc = acc + row_ror<2>(acc);
+    float sum = acc + row_ror<1>(acc);
+    if (tid == 0) {
+      for (int u = n16; u < n; u++) sum += lds[(u & 15) * S + (u >> 4)];
+      red[nw] = 1.0f / sum;
+    }
+  }
+  __syncthreads();
+  const float inv = red[nw];
+
+  float wm = 0.0f;
+  for (int u = tid; u < n; u += T) {
+    const int t = G.st + u, slot = G.ring ? t % G.ring : t;
+    wm = __builtin_fmaxf(wm, (lds[(u & 15) * S + (u >> 4)] * inv) * G.vs[slot]);
+  }
+  wm = block_max(wm, red);
+  const bool pos = wm > 0.0f;
+  const float wq_inv = 65535.0f / wm;
+
+  // weight planes for every slot of the P.V domain, four slots per thread
+  int8_t* wp = a.wpl + (size_t)(r * a.kvh + g) * a.wpl_blocks * (48 * grp) + hl * 16;
+  const int dom_hi = G.dom_lo + 64 * G.dom_steps;
+  for (int s4 = G.dom_lo + 4 * tid; s4 < dom_hi; s4 += 4 * T) {
+    uint32_t pa = 0, pb = 0, pc = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int s = s4 + e;
+      int W = 0;
+      const int mult = (s >= G.lo0 && s < G.hi0) + (G.nrun == 2 && s >= G.lo1 && s < G.hi1);
+      if (pos && mult) {
+        int t;
+        bool ok;
+        if (!G.ring) {
+          t = s, ok = s >= G.st && s < G.en;
+        } else {  // the latest position of the range held in slot s
+          const int d = ((G.en - 1 - s) % G.ring + G.ring) % G.ring;
+          t = G.en - 1 - d, ok = s < G.ring && t >= G.st;
+        }
+        if (ok) {
+          const int u = t - G.st;
+          const float wt = (lds[(u & 15) * S + (u >> 4)] * inv) * G.vs[s];
+          int q = (int)__builtin_fmaf(wt, wq_inv, 0.5f);
+          q = q > 65535 ? 65535 : (q < 0 ? 0 : q);
+          W = mult * q;
+        }
+      }
+      pa |= (uint32_t)(W >> 14) << (8 * e);
+      pb |= (uint32_t)((W >> 7) & 127) << (8 * e);
+      pc |= (uint32_t)(W & 127) << (8 * e);
+    }
+    int8_t* p = wp + (size_t)((s4 - G.dom_lo) >> 4) * (48 * grp) + (s4 & 15);
+    *(uint32_t*)p = pa;
+    *(uint32_t*)(p + 16 * grp) = pb;
+    *(uint32_t*)(p + 32 * grp) = pc;
+  }
+  int32_t* acc = a.acc + ((size_t)r * a.nh + h) * a.hd;
+  for (int i = tid; i < a.hd; i += T) acc[i] = 0;
+  if (tid == 0) {
+    a.wq[r * a.nh + h] = pos ? wm / 65535.0f : 0.0f;
+    if (h == max(a.h0, g * grp)) a.cnt[r * a.kvh + g] = 0;
+  }
+}
+
+// ------------------------------------------------------------------ 3. P.V
+// grid (p3_chunks, hd / 64, m * kvh), 256 threads: workgroup (x, y) takes the
+// slots [dom_lo + 256 x, + 256) and dims [64 y, + 64); wave w one 64-slot
+// step, all four 16-dim tiles, all three planes.
+__global__ __launch_bounds__(256) void attn_pv_kernel(const AttnArgs a) {
+  __shared__ int32_t red[4][16][64];
+  __shared__ int last;
+  const int r = blockIdx.z / a.kvh, g = blockIdx.z - r * a.kvh;
+  const Geo G = row_geo(a, r);
+  const int grp = a.nh / a.kvh;
+  const int hb = max(a.h0, g * grp), he = min(a.h1, (g + 1) * grp);
+  if (hb >= he) return;
+  const int nchunk = max(1, (G.dom_steps + 3) >> 2);
+  if ((int)blockIdx.x >= nchunk) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int kvd = a.kvh * a.hd, d0 = 64 * blockIdx.y;
+  const int step = (int)blockIdx.x * 4 + w;
+  v4i D[3][4];
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) D[p][nt] = v4i{0, 0, 0, 0};
+  if (step < G.dom_steps) {
+    const int s0 = G.dom_lo + 64 * step;
+    const int hl = lane & 15, q4 = lane >> 4;
+    const int h = g * grp + hl;
+    const bool live = hl < grp && h >= hb && h < he;
+    // A: plane p, row hl, the 16 slots s0 + 16 q4 + [0, 16)
+    const int8_t* wp = a.wpl + ((size_t)(r * a.kvh + g) * a.wpl_blocks + ((s0 - G.dom_lo) >> 4) + q4) *
+                                   (48 * grp) + hl * 16;
+    v4i A[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) A[p] = live ? *(const v4i*)(wp + p * 16 * grp) : v4i{0, 0, 0, 0};
+    // B: dim d0 + 16 nt + hl; dword q = the four slots of group s0 / 4 + 4 q4 + q
+    const int ngroups = (G.k_len + 3) >> 2;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(G.vc, (uint32_t)((size_t)ngroups * kvd * 4));
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const int j = g * a.hd + d0 + 16 * nt + hl;
+      v4i B;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int gi = (s0 >> 2) + 4 * q4 + q;
+        B[q] = buf_load_b32(rv, gi < ngroups ? ((uint32_t)gi * (uint32_t)kvd + (uint32_t)j) * 4u : FGM_OOB, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < 3; p++) D[p][nt] = mfma16(A[p], B, D[p][nt]);
+    }
+  }
+  // sum iw v = a 2^14 + b 2^7 + c (modulo 2^32, as the reference's int32 lanes)
+#pragma unroll
+  for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      red[w][4 * (lane >> 4) + i][16 * nt + (lane & 15)] =
+          (int32_t)(((uint32_t)D[0][nt][i] << 14) + ((uint32_t)D[1][nt][i] << 7) + (uint32_t)D[2][nt][i]);
+  __syncthreads();
+  for (int idx = tid; idx < 16 * 64; idx += 256) {
+    const int hl = idx >> 6, d = idx & 63, h = g * grp + hl;
+    if (hl < grp && h >= hb && h < he) {
+      const uint32_t s = (uint32_t)red[0][hl][d] + (uint32_t)red[1][hl][d] + (uint32_t)red[2][hl][d] +
+                         (uint32_t)red[3][hl][d];
+      if (s) atomicAdd(a.acc + ((size_t)r * a.nh + h) * a.hd + d0 + d, (int)s);
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t total = (uint32_t)nchunk * (uint32_t)(a.hd >> 6);
+    last = atomicAdd(a.cnt + r * a.kvh + g, 1u) == total - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int idx = tid; idx < (he - hb) * a.hd; idx += 256) {
+    const int h = hb + idx / a.hd, i = idx - (h - hb) * a.hd;
+    const size_t o = ((size_t)r * a.nh + h) * a.hd + i;
+    const int v = __hip_atomic_load(a.acc + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.out[o] = (float)v * a.wq[r * a.nh + h];
+  }
+}
+
+// ----------------------------------------------------------- cache writes
+// fgm_store_v_t (ops.c:653-657)
+__global__ void store_v_t_kernel(int8_t* vt, const int8_t* src, int n, int slot) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < n) vt[((size_t)(slot >> 2) * n + j) * 4 + (slot & 3)] = src[j];
+}
+
+// The forward pass's append (forward.rs:515-548): quant_act of each K and V
+// row (ops.c:181-204: s = amax == 0 ? 1 : amax / 127, q = cvt(x * (1 / s))
+// saturated, the n % 16 tail as lrintf + clamp), K stored in place, V through
+// the transposed layout.  grid (m, 2): y = 0 K, 1 V; 256 threads.
+constexpr int KV_VMAX = 8;  // row_len <= 4 * 256 * KV_VMAX
+__global__ __launch_bounds__(256) void kv_store_kernel(const float* k, const float* v, int rl,
+                                                      int8_t* kc, float* ks, int8_t* vt, float* vs,
+                                                      int pos0, int ring) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, isv = blockIdx.y, tid = threadIdx.x;
+  const float* src = (isv ? v : k) + (size_t)r * rl;
+  const int pos = pos0 + r, slot = ring ? pos % ring : pos;
+  float x[KV_VMAX][4];
+  float mx = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KV_VMAX; s++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = 4 * (tid + 256 * s) + e;
+      x[s][e] = c < rl ? src[c] : 0.0f;
+      mx = __builtin_fmaxf(mx, __builtin_fabsf(x[s][e]));
+    }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+  const float sc = mx == 0.0f ? 1.0f : mx / 127.0f;
+  const float inv = 1.0f / sc;
+  const int rv = rl & ~15;
+#pragma unroll
+  for (int s = 0; s < KV_VMAX; s++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = 4 * (tid + 256 * s) + e;
+      if (c >= rl) continue;
+      const float y = x[s][e] * inv;
+      const int8_t q = c < rv ? quant_vec(y) : quant_tail(y);
+      if (isv)
+        vt[((size_t)(slot >> 2) * rl + c) * 4 + (slot & 3)] = q;
+      else
+        kc[(size_t)slot * rl + c] = q;
+    }
+  if (tid == 0) (isv ? vs : ks)[slot] = sc;
+}
+
+template <int KS>
+hipError_t launch_scores(const AttnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(attn_scores_kernel<KS>, dim3(a.p1_chunks, a.m * a.kvh), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t fgm_attn_layout(AttnArgs* a, void* base, int m, int nh, int kvh, int hd, int max_span) {
+  const int grp = nh / kvh;
+  const int sc_stride = (max_span + 63) / 64 * 64;
+  // a domain spans at most max_span + 3 slots from a 64-aligned start
+  const int wpl_blocks = ((max_span + 3 + 63) / 64 + 1) * 4;
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  size_t off = 0;
+  const size_t o_sc = off;
+  off = al(off + (size_t)m * nh * sc_stride * 4);
+  const size_t o_wpl = off;
+  off = al(off + (size_t)m * kvh * wpl_blocks * 48 * grp);
+  const size_t o_acc = off;
+  off = al(off + (size_t)m * nh * hd * 4);
+  const size_t o_wq = off;
+  off = al(off + (size_t)m * nh * 4);
+  const size_t o_cnt = off;
+  off = al(off + (size_t)m * kvh * 4);
+  if (a && base) {
+    char* b = (char*)base;
+    a->sc = (float*)(b + o_sc);
+    a->sc_stride = sc_stride;
+    a->wpl = (int8_t*)(b + o_wpl);
+    a->wpl_blocks = wpl_blocks;
+    a->acc = (int32_t*)(b + o_acc);
+    a->wq = (float*)(b + o_wq);
+    a->cnt = (uint32_t*)(b + o_cnt);
+  }
+  return off;
+}
+
+hipError_t fgm_launch_attn(const AttnArgs& a, int max_n, hipStream_t st) {
+  if (a.m <= 0 || a.h1 <= a.h0) return hipSuccess;
+  hipError_t e = hipSuccess;
+  if (max_n > 0) {
+    switch (a.hd / 64) {
+      case 1: e = launch_scores<1>(a, st); break;
+      case 2: e = launch_scores<2>(a, st); break;
+      case 3: e = launch_scores<3>(a, st); break;
+      case 4: e = launch_scores<4>(a, st); break;
+      case 5: e = launch_scores<5>(a, st); break;
+      case 6: e = launch_scores<6>(a, st); break;
+      case 7: e = launch_scores<7>(a, st); break;
+      case 8: e = launch_scores<8>(a, st); break;
+      default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+  }
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_softmax_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const int T = max_n <= 2048 ? 256 : (max_n <= 8192 ? 512 : 1024);
+  const int S = (((max_n + 15) >> 4) + 16 + 63) / 64 * 64 + 4;
+  const size_t lds = ((size_t)16 * S + 32) * 4;
+  hipLaunchKernelGGL(attn_softmax_kernel, dim3(a.m * (a.h1 - a.h0)), dim3(T), lds, st, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_pv_kernel, dim3(a.p3_chunks, a.hd / 64, a.m * a.kvh), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t fgm_launch_store_v_t(int8_t* vt, const int8_t* src, int n, int slot, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(store_v_t_kernel, dim3((n + 255) / 256), dim3(256), 0, st, vt, src, n, slot);
+  return hipGetLastError();
+}
+
+hipError_t fgm_launch_kv_store(const float* k, const float* v, int m, int row_len, int8_t* kc,
+                               float* ks, int8_t* vt, float* vs, int pos0, int ring, hipStream_t st) {
+  if (m <= 0 || row_len <= 0) return hipSuccess;
+  if (row_len > 4 * 256 * KV_VMAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kv_store_kernel, dim3(m, 2), dim3(256), 0, st, k, v, row_len, kc, ks, vt, vs,
+                     pos0, ring);
+  return hipGetLastError();
+}

@@ -67,3 +67,77 @@ hipError_t fgm_launch_gelu(float* out, const float* gate, const float* up, int n
 hipError_t fgm_launch_softcap(float* x, int n, float cap, hipStream_t st);
 hipError_t fgm_launch_rope(float* x, int rows, int n_heads, int head_dim, const float* cs, hipStream_t st);
 hipError_t fgm_launch_binop(float* a, const float* b, int n, int op, float s, hipStream_t st);
+
+// int8-KV attention (fgm_attn.hip).  Rows are grouped into sequences: rows
+// [row0, row0 + nrows) of one sequence read one layer cache and sit at
+// positions pos0, pos0 + 1, ...; a row at position p attends [st, p + 1) with
+// st = window > 0 ? max(p + 1 - window, 0) : lo.  q and out are
+// [m][n_heads][head_dim]; only heads [h0, h1) are computed and written.
+constexpr int FGM_ATTN_MAX_SEQ = 16;
+constexpr int FGM_ATTN_MAX_SPAN = 32768;  // positions per row (softmax row in LDS)
+struct AttnSeq {
+  const int8_t* kc;   // [k_len][kv_heads * head_dim]
+  const float* ks;    // [k_len]
+  const int8_t* vc;   // transposed, [ceil(k_len / 4)][kv_heads * head_dim][4]
+  const float* vs;    // [k_len]
+  int k_len, ring, pos0, lo, nrows, row0;
+};
+struct AttnArgs {
+  AttnSeq seq[FGM_ATTN_MAX_SEQ];
+  int nseq, m, nh, kvh, hd, window, h0, h1;
+  float* out;
+  const float* q;
+  // scratch
+  float* sc;          // scores / exponentials [m][nh][sc_stride]
+  int sc_stride;
+  int8_t* wpl;        // weight planes [m][kvh][wpl_blocks][3][grp][16]
+  int wpl_blocks;
+  int32_t* acc;       // [m][nh][hd]
+  float* wq;          // per (row, head) dequantisation step, 0 = zero output
+  uint32_t* cnt;      // [m][kvh] completion tickets
+  int p1_chunk;       // positions per score workgroup
+  int p1_chunks;      // score workgroups per (row, kv head) in the grid
+  int p3_chunks;      // slot chunks (256 slots) per (row, kv head) in the grid
+};
+// A row's attended range and the reference's slot runs (ops.c:560-572) as
+// four-slot-aligned spans [lo, hi); the P.V slot domain is
+// [dom_lo, dom_lo + 64 dom_steps).  Shared by the host (grid sizing) and the
+// kernels.
+struct AttnSpan {
+  int st, en, n, nrun, lo0, hi0, lo1, hi1, dom_lo, dom_steps;
+};
+__host__ __device__ inline AttnSpan attn_span(int en, int lo, int window, int ring) {
+  AttnSpan g;
+  g.en = en;
+  g.st = window > 0 ? (en - window > 0 ? en - window : 0) : lo;
+  g.n = g.en - g.st;
+  g.lo1 = g.hi1 = 0;
+  if (!ring) {
+    g.lo0 = g.st, g.hi0 = g.en, g.nrun = 1;
+  } else if (g.n >= ring) {
+    g.lo0 = 0, g.hi0 = ring, g.nrun = 1;
+  } else {
+    const int s0 = g.st % ring;
+    if (s0 + g.n <= ring) {
+      g.lo0 = s0, g.hi0 = s0 + g.n, g.nrun = 1;
+    } else {
+      g.lo0 = s0, g.hi0 = ring, g.lo1 = 0, g.hi1 = s0 + g.n - ring, g.nrun = 2;
+    }
+  }
+  g.lo0 &= ~3, g.hi0 = (g.hi0 + 3) & ~3;
+  g.lo1 &= ~3, g.hi1 = (g.hi1 + 3) & ~3;
+  g.dom_lo = (g.nrun == 2 ? 0 : g.lo0) & ~63;
+  g.dom_steps = (g.hi0 - g.dom_lo + 63) >> 6;
+  return g;
+}
+// scratch layout for `m` rows whose spans (max over rows of end - start and
+// of the ring size) are at most max_span; returns the bytes and fills the
+// scratch pointers of `a` when base != nullptr.
+size_t fgm_attn_layout(AttnArgs* a, void* base, int m, int nh, int kvh, int hd, int max_span);
+hipError_t fgm_launch_attn(const AttnArgs& a, int max_n, hipStream_t st);
+// V row scatter into the transposed cache (ops.c:653-657).
+hipError_t fgm_launch_store_v_t(int8_t* vt, const int8_t* src, int n, int slot, hipStream_t st);
+// Quantise m K and V rows (quant_act per row) into one cache at slots
+// (pos0 + r) % ring (ring 0: pos0 + r): K in place, V transposed.
+hipError_t fgm_launch_kv_store(const float* k, const float* v, int m, int row_len, int8_t* kc,
+                               float* ks, int8_t* vt, float* vs, int pos0, int ring, hipStream_t st);

@@ -335,3 +335,130 @@ def softcap(x, cap: float) -> None:
     else:
         check(lib().fgm_hip_softcap_dev(_dp(x), n, cap, _stream()))
 
+
+
+# ------------------------------------------------------ int8-KV attention
+# lib.rs:293-372, 428-438.  Host arrays go to the drop-ins (the caches are
+# uploaded per call); GPU tensors go to the device API with a scratch buffer
+# from torch's allocator.
+def attend_scratch(cap: int, head_dim: int) -> int:
+    """Floats of scratch attend_q8_heads needs for a cache of `cap` positions
+    (lib.rs:340-344)."""
+    return cap + (cap + 1) // 2 + 2 * head_dim + 64
+
+
+def rowbatch_scratch(n_heads: int, cap: int, head_dim: int) -> int:
+    """lib.rs:371-373."""
+    return int(lib().fgm_rowbatch_scratch_hip(n_heads, cap, head_dim))
+
+
+def set_scalar_wfill(on: bool) -> None:
+    """lib.rs:428-430: an A/B switch the reference's kernels no longer read."""
+    lib().fgm_set_scalar_wfill_hip(1 if on else 0)
+
+
+def _dev_scratch(nbytes: int, like):
+    import torch
+    return torch.empty(max(nbytes, 256) + 256, dtype=torch.uint8, device=like.device)
+
+
+def _aligned(t) -> int:
+    return (t.data_ptr() + 255) & ~255
+
+
+def attend_q8_heads(out, q, kc, ks, vc, vs, n_heads: int, kv_heads: int, head_dim: int,
+                    start: int, end: int, scratch, h0: int, h1: int, ring: int, cap: int) -> None:
+    """Attention of one query row over positions [start, end), heads [h0, h1)
+    (lib.rs:317-338; ops.c:378-637).  `scratch` is the reference's host
+    scratch (unused by this library; may be None)."""
+    assert ring == 0 or _len(kc) >= ring * kv_heads * head_dim
+    assert _len(vc) >= (cap + 3) // 4 * 4 * kv_heads * head_dim
+    backend()
+    if _kind(out, q, kc, ks, vc, vs) == "host":
+        lib().fgm_attend_q8_heads_hip(_hp(out), _hp(q), _hp(kc), _hp(ks), _hp(vc), _hp(vs),
+                                      n_heads, kv_heads, head_dim, start, end, None, h0, h1,
+                                      ring, cap)
+    else:
+        span = max(end - start, ring, 1)
+        nb = lib().fgm_hip_attend_scratch_bytes(1, n_heads, kv_heads, head_dim, span)
+        sc = _dev_scratch(nb, out)
+        check(lib().fgm_hip_attend_heads_dev(_dp(out), _dp(q), _dp(kc), _dp(ks), _dp(vc),
+                                             _dp(vs), n_heads, kv_heads, head_dim, start,
+                                             max(end, start), h0, h1, ring, cap, _aligned(sc),
+                                             nb, _stream()))
+        out._fgm_keep = sc
+
+
+def attend_q8(out, q, kc, ks, vc, vs, n_heads: int, kv_heads: int, head_dim: int, start: int,
+              end: int, scratch=None) -> None:
+    """lib.rs:293-309; ops.c:363-368."""
+    if _kind(out, q, kc, ks, vc, vs) == "host":
+        backend()
+        lib().fgm_attend_q8_hip(_hp(out), _hp(q), _hp(kc), _hp(ks), _hp(vc), _hp(vs), n_heads,
+                                kv_heads, head_dim, start, end, None)
+    else:
+        attend_q8_heads(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start, end,
+                        scratch, 0, n_heads, 0, max(end, 1))
+
+
+def attend_q8_row(out, q, kc, ks, vc, vs, n_heads: int, kv_heads: int, head_dim: int,
+                  start: int, end: int, scratch, ring: int, cap: int) -> None:
+    """All heads of one query row (lib.rs:353-369; ops.c:729-872): an empty
+    range zeroes every head; with one kv head at most eight heads are
+    computed, as there."""
+    if _kind(out, q, kc, ks, vc, vs) == "host":
+        backend()
+        lib().fgm_attend_q8_row_hip(_hp(out), _hp(q), _hp(kc), _hp(ks), _hp(vc), _hp(vs),
+                                    n_heads, kv_heads, head_dim, start, end, None, ring, cap)
+    else:
+        h1 = n_heads if (end - start <= 0 or kv_heads != 1) else min(n_heads, 8)
+        attend_q8_heads(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start,
+                        max(end, start), scratch, 0, h1, ring, cap)
+
+
+def store_v_t(vt, src, n: int, slot: int) -> None:
+    """One quantised V row into the transposed cache (lib.rs:432-438)."""
+    assert _len(vt) >= (slot // 4 + 1) * n * 4 and _len(src) >= n
+    backend()
+    if _kind(vt, src) == "host":
+        lib().fgm_store_v_t_hip(_hp(vt), _hp(src), n, slot)
+    else:
+        check(lib().fgm_hip_store_v_t_dev(_dp(vt), _dp(src), n, slot, _stream()))
+
+
+def attend(out, q, seqs, n_heads: int, kv_heads: int, head_dim: int, window: int = 0,
+           scratch=None) -> None:
+    """Device API only: the reference's AttnJob (pool.rs:36-65) in one call.
+
+    `seqs`: list of (kc, ks, vc, vs, k_len, ring, pos, rows) with GPU tensors
+    for the caches; sequence i owns the next `rows` rows of q / out
+    ([rows][n_heads][head_dim]) at positions pos, pos + 1, ...  `scratch`: a
+    uint8 GPU tensor of at least attend_scratch_bytes(...) + 256 bytes, or None
+    to allocate one."""
+    import fastgemma_amd as F
+    backend()
+    arr = (F.AttnSeq * max(len(seqs), 1))()
+    rows, span = 0, 1
+    for i, (kc, ks, vc, vs, k_len, ring, pos, nr) in enumerate(seqs):
+        arr[i] = F.AttnSeq(_dp(kc), _dp(ks), _dp(vc), _dp(vs), k_len, ring, pos, nr)
+        rows += nr
+        span = max(span, ring, min(pos + nr, window) if window > 0 else pos + nr)
+    nb = lib().fgm_hip_attend_scratch_bytes(max(rows, 1), n_heads, kv_heads, head_dim, span)
+    sc = scratch if scratch is not None else _dev_scratch(nb, out)
+    check(lib().fgm_hip_attend_dev(_dp(out), _dp(q), arr, len(seqs), n_heads, kv_heads, head_dim,
+                                   window, _aligned(sc), nb, _stream()))
+    out._fgm_keep = sc
+
+
+def attend_scratch_bytes(rows: int, n_heads: int, kv_heads: int, head_dim: int,
+                         max_span: int) -> int:
+    return int(lib().fgm_hip_attend_scratch_bytes(rows, n_heads, kv_heads, head_dim, max_span))
+
+
+def kv_store(k, v, m: int, row_len: int, kc, ks, vt, vs, cap: int, pos: int,
+             ring: int = 0) -> None:
+    """Device API only: quantise m K / V rows into a layer cache of `cap`
+    slots at positions pos .. pos + m - 1 (forward.rs:515-548)."""
+    backend()
+    check(lib().fgm_hip_kv_store_dev(_dp(k), _dp(v), m, row_len, _dp(kc), _dp(ks), _dp(vt),
+                                     _dp(vs), cap, pos, ring, _stream()))

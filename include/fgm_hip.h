@@ -159,6 +159,75 @@ int fgm_hip_add_dev(float *a, const float *b, int n, void *stream);
 int fgm_hip_mul_dev(float *a, const float *b, int n, void *stream);
 int fgm_hip_scale_dev(float *a, float s, int n, void *stream);
 
+/* ------------------------------------------------------ int8-KV attention
+ * The forward pass's attention over the int8 KV cache (ops.c:353-877,
+ * kv.rs).  Cache layout per layer (kv.rs:13-50): K [k_len][kv_heads *
+ * head_dim] int8 with one f32 scale per slot; V transposed in groups of four
+ * slots, vt[((slot/4) * kvd + j) * 4 + slot%4], with one scale per slot;
+ * slot = ring ? pos % ring : pos.  q and out are [rows][n_heads][head_dim] f32.
+ * Results equal the reference's bytes; the only operation evaluated
+ * differently is exp on the n % 16 tail of the softmax (libm expf there,
+ * correctly rounded here; they differ where glibc's expf is not correctly
+ * rounded).  Limits: head_dim a multiple of 64 up to 512, at most 16 query
+ * heads per kv head, at most 32768 positions per row, a ring range no longer
+ * than the ring (the reference's scratch layout assumes it too). */
+
+/* drop-ins, host pointers, same parameters as the reference's symbols; the
+ * caches are uploaded per call, `scratch` is not touched */
+void fgm_attend_q8_hip(float *out, const float *q, const int8_t *kc, const float *ks,
+                       const int8_t *vc, const float *vs, int n_heads, int kv_heads, int head_dim,
+                       int start, int end, float *scratch);               /* lib.rs:60-64, ops.c:363-368 */
+void fgm_attend_q8_heads_hip(float *out, const float *q, const int8_t *kc, const float *ks,
+                             const int8_t *vc, const float *vs, int n_heads, int kv_heads,
+                             int head_dim, int start, int end, float *scratch, int h0, int h1,
+                             int ring, int cap);                           /* lib.rs:65-70, ops.c:378-637 */
+void fgm_attend_q8_row_hip(float *out, const float *q, const int8_t *kc, const float *ks,
+                           const int8_t *vc, const float *vs, int n_heads, int kv_heads,
+                           int head_dim, int start, int end, float *scratch, int ring,
+                           int cap);                                       /* lib.rs:73-78, ops.c:729-872 */
+void fgm_store_v_t_hip(int8_t *vt, const int8_t *src, int n, int slot);  /* lib.rs:71, ops.c:653-657 */
+void fgm_set_scalar_wfill_hip(int on);                                  /* lib.rs:72, ops.c:53-54 (no effect there either) */
+int fgm_rowbatch_scratch_hip(int n_heads, int cap, int head_dim);       /* lib.rs:79, ops.c:875-877 */
+
+/* device API.  One call covers the rows of up to 16 sequences (the
+ * reference's AttnJob, pool.rs:36-65): sequence i owns the next `rows` rows
+ * of q / out, at positions pos, pos + 1, ..., and reads one layer cache of
+ * k_len slots (ring: ring-buffer capacity, 0 = linear).  A row at position p
+ * attends [max(p + 1 - window, 0), p + 1) (window 0: [0, p + 1)), all heads,
+ * kv head h / (n_heads / kv_heads).  `scratch`: device memory, 256-byte
+ * aligned, at least fgm_hip_attend_scratch_bytes(total rows, ..., max_span)
+ * where max_span bounds every row's range length and every ring size.  The
+ * scratch is used during the call only (calls on one scratch buffer must not
+ * overlap). */
+typedef struct fgm_hip_attn_seq {
+  const int8_t *kc;
+  const float *ks;
+  const int8_t *vc;
+  const float *vs;
+  int k_len;
+  int ring;
+  int pos;
+  int rows;
+} fgm_hip_attn_seq;
+
+size_t fgm_hip_attend_scratch_bytes(int rows, int n_heads, int kv_heads, int head_dim, int max_span);
+int fgm_hip_attend_dev(float *out, const float *q, const fgm_hip_attn_seq *seqs, int nseq,
+                       int n_heads, int kv_heads, int head_dim, int window, void *scratch,
+                       size_t scratch_bytes, void *stream);
+/* fgm_attend_q8_heads on device pointers: one row, range [start, end), heads
+ * [h0, h1) (the others are not written) */
+int fgm_hip_attend_heads_dev(float *out, const float *q, const int8_t *kc, const float *ks,
+                             const int8_t *vc, const float *vs, int n_heads, int kv_heads,
+                             int head_dim, int start, int end, int h0, int h1, int ring, int cap,
+                             void *scratch, size_t scratch_bytes, void *stream);
+int fgm_hip_store_v_t_dev(int8_t *vt, const int8_t *src, int n, int slot, void *stream);
+/* The forward pass's cache append (forward.rs:515-548): rows r < m of k and v
+ * (f32 [m][row_len]) quantised as fgm_quant_act does, K to kc[slot], V to vt
+ * transposed, scales to ks / vs, slot = ring ? (pos + r) % ring : pos + r;
+ * cap: slots the cache holds (checked). */
+int fgm_hip_kv_store_dev(const float *k, const float *v, int m, int row_len, int8_t *kc, float *ks,
+                         int8_t *vt, float *vs, int cap, int pos, int ring, void *stream);
+
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);

@@ -85,6 +85,13 @@ def lib() -> C.CDLL:
         L.orc_mul.argtypes = [_p, _p, _i]
         L.orc_scale.argtypes = [_p, _f, _i]
         L.orc_softcap.argtypes = [_p, _i, _f]
+        L.orc_attend_q8_heads.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i,
+                                          _i, _i]
+        L.orc_attend_q8.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i]
+        L.orc_attend_q8_row.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i]
+        L.orc_store_v_t.argtypes = [_p, _p, _i, _i]
+        L.orc_rowbatch_scratch.restype = _i
+        L.orc_rowbatch_scratch.argtypes = [_i, _i, _i]
         L.orc_xorshift_fill.restype = _u64
         L.orc_xorshift_fill.argtypes = [_u64, _sz, _i, _i, _p]
         L.orc_lcg_fill.restype = C.c_uint32
@@ -117,6 +124,13 @@ def _bind_ref(L: C.CDLL) -> None:
     L.fgm_mul.argtypes = [_p, _p, _i]
     L.fgm_scale.argtypes = [_p, _f, _i]
     L.fgm_softcap.argtypes = [_p, _i, _f]
+    L.fgm_attend_q8.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]
+    L.fgm_attend_q8_heads.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i, _i,
+                                      _i, _i]
+    L.fgm_attend_q8_row.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i, _i]
+    L.fgm_store_v_t.argtypes = [_p, _p, _i, _i]
+    L.fgm_rowbatch_scratch.restype = _i
+    L.fgm_rowbatch_scratch.argtypes = [_i, _i, _i]
 
 
 def ref() -> C.CDLL | None:
@@ -389,3 +403,89 @@ def softcap(x: np.ndarray, cap: float) -> np.ndarray:
     lib().orc_softcap(_ptr(out), out.size, cap)
     return out
 
+
+
+# ------------------------------------------------------ int8-KV attention
+class KvLayer:
+    """One layer's int8 KV cache in the reference's layout (kv.rs:13-50):
+    kc [cap][kvd] int8, ks [cap] f32, vt transposed in groups of four slots
+    ([ceil(cap/4)][kvd][4] int8), vs [cap] f32."""
+
+    def __init__(self, cap: int, kv_heads: int, head_dim: int):
+        self.cap, self.kvh, self.hd = cap, kv_heads, head_dim
+        kvd = kv_heads * head_dim
+        self.kc = np.zeros(cap * kvd, np.int8)
+        self.ks = np.zeros(cap, np.float32)
+        self.vt = np.zeros((cap + 3) // 4 * 4 * kvd, np.int8)
+        self.vs = np.zeros(cap, np.float32)
+
+    def store(self, slot: int, krow: np.ndarray, vrow: np.ndarray) -> None:
+        """The forward pass's write (forward.rs:515-548): quant_act each row,
+        K in place, V through store_v_t."""
+        kvd = self.kvh * self.hd
+        q, s = quant_act(krow, 1, kvd)
+        self.kc[slot * kvd:(slot + 1) * kvd] = q[0]
+        self.ks[slot] = s[0]
+        q, s = quant_act(vrow, 1, kvd)
+        store_v_t(self.vt, q[0], slot)
+        self.vs[slot] = s[0]
+
+
+def store_v_t(vt: np.ndarray, src: np.ndarray, slot: int) -> None:
+    src = np.ascontiguousarray(src, np.int8)
+    lib().orc_store_v_t(_ptr(vt), _ptr(src), src.size, slot)
+
+
+def tail_noncr() -> int:
+    """Tail expf values (since the last reset) that were not the correctly
+    rounded exp."""
+    return C.c_int.in_dll(lib(), "orc_attn_tail_noncr").value
+
+
+def reset_tail_noncr() -> None:
+    C.c_int.in_dll(lib(), "orc_attn_tail_noncr").value = 0
+
+
+def attend_heads(q, kv: KvLayer, n_heads: int, start: int, end: int, h0: int = 0,
+                 h1: int | None = None, ring: int = 0, out=None) -> np.ndarray:
+    """fgm_attend_q8_heads (ops.c:378-637) on a KvLayer; out [n_heads * hd]
+    (heads outside [h0, h1) keep `out`'s values)."""
+    h1 = n_heads if h1 is None else h1
+    q = _f32(q)
+    out = np.zeros(n_heads * kv.hd, np.float32) if out is None else out
+    lib().orc_attend_q8_heads(_ptr(out), _ptr(q), _ptr(kv.kc), _ptr(kv.ks), _ptr(kv.vt),
+                              _ptr(kv.vs), n_heads, kv.kvh, kv.hd, start, end, h0, h1, ring,
+                              kv.cap)
+    return out
+
+
+def attend_row(q, kv: KvLayer, n_heads: int, start: int, end: int, ring: int = 0,
+               out=None) -> np.ndarray:
+    """fgm_attend_q8_row (ops.c:729-872)."""
+    q = _f32(q)
+    out = np.zeros(n_heads * kv.hd, np.float32) if out is None else out
+    lib().orc_attend_q8_row(_ptr(out), _ptr(q), _ptr(kv.kc), _ptr(kv.ks), _ptr(kv.vt),
+                            _ptr(kv.vs), n_heads, kv.kvh, kv.hd, start, end, ring, kv.cap)
+    return out
+
+
+def ref_attend(kind: str, q, kv: KvLayer, n_heads: int, start: int, end: int, h0: int = 0,
+               h1: int | None = None, ring: int = 0, out=None) -> np.ndarray | None:
+    """The reference's own fgm_attend_q8{,_heads,_row} (oracle/_ref), or None."""
+    R = ref()
+    if R is None:
+        return None
+    h1 = n_heads if h1 is None else h1
+    q = _f32(q)
+    out = np.zeros(n_heads * kv.hd, np.float32) if out is None else out
+    scratch = np.zeros(R.fgm_rowbatch_scratch(n_heads, kv.cap, kv.hd) + 4 * kv.cap + 256,
+                       np.float32)
+    args = (_ptr(out), _ptr(q), _ptr(kv.kc), _ptr(kv.ks), _ptr(kv.vt), _ptr(kv.vs), n_heads,
+            kv.kvh, kv.hd, start, end, _ptr(scratch))
+    if kind == "q8":
+        R.fgm_attend_q8(*args)
+    elif kind == "heads":
+        R.fgm_attend_q8_heads(*args, h0, h1, ring, kv.cap)
+    else:
+        R.fgm_attend_q8_row(*args, ring, kv.cap)
+    return out

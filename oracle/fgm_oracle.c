@@ -561,3 +561,178 @@ void orc_softcap(float *x, int n, float cap) {
     }
   }
 }
+
+/* ------------------------------------------------------ int8-KV attention
+ * fgm_attend_q8_heads / fgm_attend_q8_row / fgm_store_v_t (ops.c:353-877).
+ * Caches: K [cap][kv_heads * head_dim] int8 with one f32 scale per slot; V
+ * transposed in groups of four slots, vt[((slot/4) * kvd + j) * 4 + slot%4]
+ * (ops.c:645-657, kv.rs:20-31); slot = ring ? t % ring : t.
+ *
+ * The integer parts (Q.K dot products, P.V accumulators) are exact, so any
+ * summation order gives the reference's values; the float parts follow the
+ * reference's order: score = ((float)dot * qscale) * kscale; exp of the
+ * 16-wide chunks by exp512_ps with 16 lane sums (plain adds, chunk order) and
+ * GCC's reduce tree, the n % 16 tail by libm expf added in order; weights
+ * ((e * inv) * vs) with a 16-bit quantisation iw = (int)(w * wq_inv + 0.5f)
+ * (GCC contracts the multiply-add into one fma at -O2 -march=cascadelake);
+ * out = (float)(sum iw * v) * wq_scale.
+ *
+ * orc_attn_tail_noncr counts tail expf values that differ from the correctly
+ * rounded exp (the GPU evaluates the tail correctly rounded); tests read it to
+ * know when the tail can be compared bit for bit. */
+int orc_attn_tail_noncr = 0;
+
+static void orc_attn_head(float *oh, const float *qh, const int8_t *kc, const float *ks,
+                          const int8_t *vc, const float *vs, int kvd, int kv_off, int head_dim,
+                          int start, int end, int ring) {
+  /* per-head int8 query (ops.c:417-433) */
+  int8_t qq[512];
+  float qamax = 0.0f;
+  for (int i = 0; i < head_dim; i++) {
+    const float a = fabsf(qh[i]);
+    if (a > qamax) qamax = a;
+  }
+  const float qscale = qamax / 127.0f;
+  const float qinv = qamax > 0.0f ? 127.0f / qamax : 0.0f;
+  for (int i = 0; i < head_dim; i++) {
+    int v = (int)lrintf(qh[i] * qinv);
+    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    qq[i] = (int8_t)v;
+  }
+  const int n = end - start;
+  float *sc = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+  float mx = -INFINITY;
+  /* scores (ops.c:441-488): sum (k + 128) q - 128 sum q == sum k q exactly */
+  for (int t = start; t < end; t++) {
+    const int slot = ring ? t % ring : t;
+    const int8_t *kp = kc + (size_t)slot * kvd + kv_off;
+    int32_t d = 0;
+    for (int i = 0; i < head_dim; i++) d += (int32_t)kp[i] * (int32_t)qq[i];
+    const float s = (float)d * qscale * ks[slot];
+    sc[t - start] = s;
+    if (s > mx) mx = s;
+  }
+  /* softmax (ops.c:493-505) */
+  float lanes[16] = {0};
+  int u = 0;
+  for (; u + 16 <= n; u += 16)
+    for (int j = 0; j < 16; j++) {
+      const float e = orc_exp16(sc[u + j] - mx);
+      sc[u + j] = e;
+      lanes[j] = lanes[j] + e;
+    }
+  float sum = gcc_reduce_add16(lanes);
+  for (; u < n; u++) {
+    const float x = sc[u] - mx;
+    sc[u] = expf(x);
+    if (sc[u] != (float)exp((double)x)) orc_attn_tail_noncr++;
+    sum += sc[u];
+  }
+  const float inv = 1.0f / sum;
+  /* weight range (ops.c:546-550) */
+  float wmax = 0.0f;
+  for (int t = start; t < end; t++) {
+    const float w = sc[t - start] * inv * vs[ring ? t % ring : t];
+    if (w > wmax) wmax = w;
+  }
+  if (!(wmax > 0.0f)) {
+    for (int i = 0; i < head_dim; i++) oh[i] = 0.0f;
+    free(sc);
+    return;
+  }
+  const float wq_scale = wmax / 65535.0f, wq_inv = 65535.0f / wmax;
+  /* slot runs and their four-slot-aligned spans (ops.c:560-584) */
+  int run_lo[2], run_hi[2], nrun;
+  if (!ring) {
+    run_lo[0] = start; run_hi[0] = end; nrun = 1;
+  } else if (n >= ring) {
+    run_lo[0] = 0; run_hi[0] = ring; nrun = 1;
+  } else {
+    const int s0 = start % ring;
+    if (s0 + n <= ring) {
+      run_lo[0] = s0; run_hi[0] = s0 + n; nrun = 1;
+    } else {
+      run_lo[0] = s0; run_hi[0] = ring; run_lo[1] = 0; run_hi[1] = s0 + n - ring; nrun = 2;
+    }
+  }
+  int span_hi = 0;
+  for (int r = 0; r < nrun; r++) {
+    const int hi = (run_hi[r] + 3) & ~3;
+    if (hi > span_hi) span_hi = hi;
+  }
+  /* u16 weights by slot (ops.c:591-598): zero over the spans, the later t wins */
+  int32_t *iw = (int32_t *)calloc((size_t)span_hi + 4, sizeof(int32_t));
+  for (int t = start; t < end; t++) {
+    const int sl = ring ? t % ring : t;
+    const float w = sc[t - start] * inv * vs[sl];
+    int q = (int)fmaf(w, wq_inv, 0.5f);
+    if (q > 65535) q = 65535;
+    if (q < 0) q = 0;
+    iw[sl] = q;
+  }
+  /* P.V over each run's span (ops.c:605-631); a slot inside two spans counts
+   * twice, as there.  (acc_hi << 8) + acc_lo == sum iw * v modulo 2^32. */
+  uint32_t acc[512];
+  for (int i = 0; i < head_dim; i++) acc[i] = 0;
+  for (int r = 0; r < nrun; r++) {
+    const int glo = run_lo[r] & ~3, ghi = (run_hi[r] + 3) & ~3;
+    for (int s = glo; s < ghi; s++) {
+      if (!iw[s]) continue;
+      const int8_t *vp = vc + ((size_t)(s >> 2) * kvd + kv_off) * 4 + (s & 3);
+      for (int i = 0; i < head_dim; i++) acc[i] += (uint32_t)(iw[s] * (int32_t)vp[(size_t)i * 4]);
+    }
+  }
+  for (int i = 0; i < head_dim; i++) oh[i] = (float)(int32_t)acc[i] * wq_scale;
+  free(iw);
+  free(sc);
+}
+
+/* fgm_attend_q8_heads (ops.c:378-637): heads [h0, h1); kv head h / (n_heads /
+ * kv_heads) */
+void orc_attend_q8_heads(float *out, const float *q, const int8_t *kc, const float *ks,
+                         const int8_t *vc, const float *vs, int n_heads, int kv_heads,
+                         int head_dim, int start, int end, int h0, int h1, int ring, int cap) {
+  (void)cap;
+  const int kvd = kv_heads * head_dim, grp = n_heads / kv_heads;
+  for (int h = h0; h < h1; h++)
+    orc_attn_head(out + (size_t)h * head_dim, q + (size_t)h * head_dim, kc, ks, vc, vs, kvd,
+                  (h / grp) * head_dim, head_dim, start, end, ring);
+}
+
+/* fgm_attend_q8 (ops.c:363-368) */
+void orc_attend_q8(float *out, const float *q, const int8_t *kc, const float *ks,
+                   const int8_t *vc, const float *vs, int n_heads, int kv_heads, int head_dim,
+                   int start, int end) {
+  orc_attend_q8_heads(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start, end, 0,
+                      n_heads, 0, end);
+}
+
+/* fgm_attend_q8_row (ops.c:729-872): n <= 0 zeroes every head; kv_heads != 1
+ * takes the per-head path; otherwise at most 8 heads are computed (heads past
+ * the eighth are left untouched), with the per-head numerics. */
+void orc_attend_q8_row(float *out, const float *q, const int8_t *kc, const float *ks,
+                       const int8_t *vc, const float *vs, int n_heads, int kv_heads,
+                       int head_dim, int start, int end, int ring, int cap) {
+  if (end - start <= 0) {
+    for (int i = 0; i < n_heads * head_dim; i++) out[i] = 0.0f;
+    return;
+  }
+  if (kv_heads != 1) {
+    orc_attend_q8_heads(out, q, kc, ks, vc, vs, n_heads, kv_heads, head_dim, start, end, 0,
+                        n_heads, ring, cap);
+    return;
+  }
+  orc_attend_q8_heads(out, q, kc, ks, vc, vs, n_heads, 1, head_dim, start, end, 0,
+                      n_heads > 8 ? 8 : n_heads, ring, cap);
+}
+
+/* fgm_store_v_t (ops.c:653-657) */
+void orc_store_v_t(int8_t *vt, const int8_t *src, int n, int slot) {
+  int8_t *dst = vt + (size_t)(slot >> 2) * n * 4 + (slot & 3);
+  for (int j = 0; j < n; j++) dst[(size_t)j * 4] = src[j];
+}
+
+/* fgm_rowbatch_scratch (ops.c:875-877) */
+int orc_rowbatch_scratch(int n_heads, int cap, int head_dim) {
+  return n_heads * cap + (cap + 3) / 2 + 2 * head_dim + 64;
+}

@@ -190,3 +190,54 @@ def rope_inputs(n_heads: int, head_dim: int):
     x = oracle.gen_normal(0xA0BE + head_dim, n_heads * head_dim)
     return x, inv
 
+
+
+# ------------------------------------------------------ int8-KV attention
+# (name, n_heads, kv_heads, head_dim, cap, ring, start, end, h0, h1, qmul, path)
+# path: "heads" = fgm_attend_q8_heads, "row" = fgm_attend_q8_row,
+# "q8" = fgm_attend_q8.  Caches are filled at every slot.
+ATTN_CASES = [
+    ("dec256_n1000", 8, 1, 256, 1024, 0, 0, 1000, 0, 8, 1.0, "heads"),
+    ("dec512_n4096", 8, 1, 512, 4096, 0, 0, 4096, 0, 8, 1.0, "heads"),
+    ("dec512_n4096_row", 8, 1, 512, 4096, 0, 0, 4096, 0, 8, 1.0, "row"),
+    ("q8_n777", 8, 1, 256, 800, 0, 0, 777, 0, 8, 1.0, "q8"),
+    ("n1", 8, 1, 256, 64, 0, 0, 1, 0, 8, 1.0, "heads"),
+    ("n15", 8, 1, 256, 64, 0, 0, 15, 0, 8, 1.0, "heads"),
+    ("n16", 8, 1, 256, 64, 0, 0, 16, 0, 8, 1.0, "heads"),
+    ("n17_off", 8, 1, 256, 64, 0, 5, 22, 0, 8, 1.0, "heads"),
+    ("win_off", 8, 1, 512, 2048, 0, 1023, 1536, 0, 8, 1.0, "heads"),
+    ("sharp", 8, 1, 256, 512, 0, 0, 512, 0, 8, 16.0, "heads"),
+    ("flat", 8, 1, 256, 512, 0, 0, 512, 0, 8, 0.01, "heads"),
+    ("heads_sub", 8, 1, 256, 512, 0, 0, 300, 2, 5, 1.0, "heads"),
+    ("gqa_kv2", 8, 2, 256, 512, 0, 0, 333, 0, 8, 1.0, "heads"),
+    ("gqa_kv2_row", 8, 2, 256, 512, 0, 0, 333, 0, 8, 1.0, "row"),
+    ("row_nh4", 4, 1, 256, 512, 0, 0, 200, 0, 4, 1.0, "row"),
+    ("row_nh12", 12, 1, 128, 256, 0, 0, 100, 0, 12, 1.0, "row"),
+    ("ring_nowrap", 8, 1, 256, 520, 520, 100, 612, 0, 8, 1.0, "heads"),
+    ("ring_wrap", 8, 1, 256, 520, 520, 1301, 1813, 0, 8, 1.0, "heads"),
+    ("ring_full", 8, 1, 256, 520, 520, 3000, 3520, 0, 8, 1.0, "heads"),
+    ("ring_gap1", 8, 1, 256, 100, 100, 150, 249, 0, 8, 1.0, "heads"),
+    ("ring_row", 8, 1, 256, 520, 520, 1301, 1813, 0, 8, 1.0, "row"),
+    ("ring_odd", 8, 1, 256, 77, 77, 60, 120, 0, 8, 1.0, "heads"),
+    ("empty", 8, 1, 256, 64, 0, 10, 10, 0, 8, 1.0, "heads"),
+    ("empty_row", 8, 1, 256, 64, 0, 10, 10, 0, 8, 1.0, "row"),
+]
+
+
+def attn_inputs(name: str, n_heads: int, kv_heads: int, head_dim: int, cap: int, qmul: float):
+    """Seeded query and cache: K, V ~ U[-1, 1) per element, quantised per slot
+    as the forward pass writes them; q ~ qmul * U[-1, 1) (qmul sets how peaked
+    the softmax is, as in the reference's bench/kernels/attn_test.c).  Head 1
+    of the query is all zeros (qamax = 0: uniform attention)."""
+    seed = sum(ord(c) * (i + 1) for i, c in enumerate(name)) & 0xFFFF
+    kvd = kv_heads * head_dim
+    kv = oracle.KvLayer(cap, kv_heads, head_dim)
+    kf = oracle.gen_uniform(0xA77E0 + seed, cap * kvd, -1.0, 1.0).reshape(cap, kvd)
+    vf = oracle.gen_uniform(0xA77E1 + seed, cap * kvd, -1.0, 1.0).reshape(cap, kvd)
+    for t in range(cap):
+        kv.store(t, kf[t], vf[t])
+    q = oracle.gen_uniform(0xA77E2 + seed, n_heads * head_dim, -1.0, 1.0) * np.float32(qmul)
+    q = q.astype(np.float32)
+    if n_heads > 1:
+        q[head_dim:2 * head_dim] = 0.0
+    return q, kv

@@ -172,6 +172,14 @@ def main() -> None:
     out["elem"] = elem
     out["rope"] = rope
 
+    attn = {}
+    for (name, nh, kvh, hd, cap, ring, st, en, h0, h1, qmul, path) in cases.ATTN_CASES:
+        q, kv = cases.attn_inputs(name, nh, kvh, hd, cap, qmul)
+        o = np.full(nh * hd, 7.0, np.float32)   # heads a call leaves alone keep 7.0
+        oracle.ref_attend(path, q, kv, nh, st, en, h0, h1, ring, out=o)
+        attn[name] = {"sha256": digest(o), "samples": samples(o)}
+    out["attn"] = attn
+
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_outputs.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
