@@ -407,6 +407,58 @@ def extra_elem(gpu):
                         "launches (a launch costs >= 1.8 us on this box)", "per_op": res}
 
 
+def extra_attn(gpu):
+    """int8-KV attention (the forward pass's other hot loop, ops.c:353-877),
+    one fgm_hip_attend_dev call (three launches) per layer: batched decode of
+    8 sequences and a 256-row prefill chunk, full attention (head_dim 512,
+    8192 positions) and sliding (head_dim 256, window 512, ring 520); 8 query
+    heads on one kv head.  Bytes = K and V bytes (+ scales) each row reads."""
+    import numpy as np
+    from fastgemma_amd import kernels
+    t = gpu.t
+    res = {}
+    nh = 8
+
+    def cache(cap, hd, copies):
+        out = []
+        for _ in range(copies):
+            kc = t.randint(-127, 128, (cap * hd,), dtype=t.int8, device=gpu.dev)
+            vt = t.randint(-127, 128, ((cap + 3) // 4 * 4 * hd,), dtype=t.int8, device=gpu.dev)
+            ks = t.rand(cap, device=gpu.dev) * 0.01 + 0.001
+            vs = t.rand(cap, device=gpu.dev) * 0.01 + 0.001
+            out.append((kc, ks, vt, vs))
+        return out
+
+    for name, hd, cap, ring, window, nseq, rows, pos in (
+            ("decode full M=8 ctx 8192 hd 512", 512, 8192, 0, 0, 8, 1, 8191),
+            ("decode sliding M=8 win 512 hd 256", 256, 520, 520, 512, 8, 1, 20000),
+            ("prefill full 256 rows ctx 8192 hd 512", 512, 8192, 0, 0, 1, 256, 7936),
+            ("prefill sliding 256 rows win 512 hd 256", 256, 768, 768, 512, 1, 256, 20000)):
+        copies = 2 if nseq == 1 else 1
+        caches = [cache(cap, hd, copies) for _ in range(nseq)]
+        m = nseq * rows
+        q = t.randn(m * nh * hd, device=gpu.dev)
+        out = t.empty(m * nh * hd, device=gpu.dev)
+        span = max(ring, window if window else pos + rows)
+        nb = kernels.attend_scratch_bytes(m, nh, 1, hd, span)
+        scratch = t.empty(nb + 256, dtype=t.uint8, device=gpu.dev)
+        nbytes = 0
+        for r in range(rows):
+            en = pos + r + 1
+            n = min(en, window) if window else en
+            nbytes += n * (2 * hd + 8)
+        nbytes *= nseq
+
+        def call(i):
+            seqs = [(c[i % copies][0], c[i % copies][1], c[i % copies][2], c[i % copies][3], cap,
+                     ring, pos, rows) for c in caches]
+            kernels.attend(out, q, seqs, nh, 1, hd, window, scratch=scratch)
+        dt = kernel_avg(gpu, call, 8, 3)
+        res[name] = {"us": dt * 1e6, "GB_s": nbytes / dt / 1e9, "frac_hbm": nbytes / dt / HBM_PEAK,
+                     "kv_bytes": nbytes}
+    return {"workload": "attention per layer call, graphs of 8 calls", "per_case": res}
+
+
 # ------------------------------------------------------------ CPU baseline
 def cpu_baseline(host, budget_s=10.0):
     import numpy as np
@@ -492,6 +544,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default=None,
+                    help="run one extra measurement (cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
+                         "attn) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -501,6 +556,15 @@ def main():
 
     gpu = Gpu()
     gpu.t.manual_seed(1234)
+    extras = {"cfg1": extra_cfg1, "int4_stream": extra_int4_stream, "cfg3": extra_cfg3,
+              "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem, "attn": extra_attn}
+    if args.only is not None:
+        if args.only not in extras:
+            print(f"--only: unknown measurement {args.only!r} (one of {', '.join(extras)})",
+                  file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({args.only: extras[args.only](gpu)}))
+        return
     log("setting up cfg2 (48 weight copies)")
     step, gemv_pair, gemv_up, gemv_down, step_bytes, host = cfg2_setup(gpu)
 
@@ -534,9 +598,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        for name, fn in (("cfg1", extra_cfg1), ("int4_stream", extra_int4_stream),
-                         ("cfg3", extra_cfg3), ("cfg5", extra_cfg5), ("cfg4", extra_cfg4),
-                         ("elem", extra_elem)):
+        for name, fn in extras.items():
             log("extra", name)
             try:
                 extra[name] = fn(gpu)

@@ -744,7 +744,7 @@ static int attn_plan(AttnArgs& a, int* max_n, int* max_span) {
   if (a.nseq < 0 || a.nseq > FGM_ATTN_MAX_SEQ)
     return fail(FGM_HIP_EINVAL, "attend: %d sequences (at most %d per call)", a.nseq, FGM_ATTN_MAX_SEQ);
   if (!a.out || !a.q) return fail(FGM_HIP_EINVAL, "attend: out or q is NULL");
-  int m = 0, mn = 0, ms = 1, p1max = 1, p3max = 1;
+  int m = 0, mn = 0, ms = 1, p1max = 1, steps_max = 1;
   long long tiles = 0;
   for (int i = 0; i < a.nseq; i++) {
     AttnSeq& s = a.seq[i];
@@ -770,17 +770,19 @@ static int attn_plan(AttnArgs& a, int* max_n, int* max_span) {
       mn = std::max(mn, sp.n);
       ms = std::max(ms, std::max(sp.n, s.ring));
       tiles += (sp.n + 15) / 16;
-      p3max = std::max(p3max, std::max(1, (sp.dom_steps + 3) / 4));
+      steps_max = std::max(steps_max, sp.dom_steps);
     }
   }
-  // positions per score workgroup: one 16-position tile per wave while the
-  // launch is small, more once it has thousands of tiles
-  const int tpw = (int)std::min<long long>(16, std::max<long long>(1, tiles / (4 * 2048)));
+  // positions per score workgroup: two 16-position tiles per wave while the
+  // launch is small (about 512 workgroups), more once it has thousands
+  const int tpw = (int)std::min<long long>(16, std::max<long long>(2, tiles / (4 * 512)));
   a.p1_chunk = 64 * tpw;
   p1max = std::max(1, (mn + a.p1_chunk - 1) / a.p1_chunk);
   a.m = m;
   a.p1_chunks = p1max;
-  a.p3_chunks = p3max;
+  // P.V: the row's 64-slot steps split into at most attn_pv_chunks chunks
+  const int chunks = m ? attn_pv_chunks(m, a.kvh, a.hd) : 1;
+  a.p3_spw = std::max(1, (steps_max + 4 * chunks - 1) / (4 * chunks));
   *max_n = mn;
   *max_span = ms;
   return FGM_HIP_OK;

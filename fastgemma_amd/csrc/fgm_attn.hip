@@ -2,7 +2,7 @@
 // fgm_attend_q8_row (ops.c:353-877), the transposed V store (ops.c:653-657)
 // and the forward pass's KV append (forward.rs:515-548).
 //
-// One call is three launches:
+// One call is four launches:
 //  1. attn_scores_kernel: s = ((float)(K.q) * qscale) * kscale for every
 //     (row, head, position).  Each workgroup makes the per-head int8 query
 //     (amax, 127 / amax, round to nearest even, clamp +-127; ops.c:417-433);
@@ -17,10 +17,11 @@
 //     (iw = a 2^14 + b 2^7 + c).  A slot's weight is multiplied by the number
 //     of the reference's four-slot-aligned run spans that contain it, since
 //     ops.c:605-631 walks each span in turn.
-//  3. attn_pv_kernel: out = (float)(sum over slots of iw v) * (wmax / 65535):
-//     the planes against the transposed V cache on v_mfma_i32_16x16x64_i8,
-//     exact int32 partial sums added with device atomics (integer addition is
-//     order-free), and the last workgroup of a (row, kv head) converts.
+//  3. attn_pv_kernel: sum over slots of iw v, the planes against the
+//     transposed V cache on v_mfma_i32_16x16x64_i8, one exact int32 partial
+//     sum per slot chunk;
+//  4. attn_final_kernel: out = (float)(sum of the partials) * (wmax / 65535)
+//     (integer addition is order-free, so the chunking changes nothing).
 // Everything that is not integer arithmetic follows the reference's
 // operation order, so outputs equal its bytes.
 #include <hip/hip_runtime.h>
@@ -127,6 +128,27 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
   if (hb >= he) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
+  const int kvd = a.kvh * HD;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(G.kc, (uint32_t)((size_t)G.k_len * kvd));
+  const int t_end = min(t_beg + a.p1_chunk, G.en);
+  float* srow = a.sc + (size_t)r * a.nh * a.sc_stride;
+  // the wave's tiles t0 = t_beg + 16 w + 64 i; a tile's K and K scale are in
+  // flight while the previous tile multiplies (the first while the query is
+  // quantised)
+  auto load = [&](v4i* B, float& kscale, int t0) {
+    const int t = t0 + (lane & 15);
+    const int slot = G.ring ? t % G.ring : t;
+    const bool ok = t < t_end;
+    const uint32_t base = ok ? (uint32_t)slot * (uint32_t)kvd + (uint32_t)(g * HD + 16 * (lane >> 4)) : FGM_OOB;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) B[kk] = buf_load_b128(rk, base, 64 * kk);
+    kscale = ok ? G.ks[slot] : 0.0f;
+  };
+  v4i B0[KS], B1[KS];
+  float ks0 = 0.0f, ks1 = 0.0f;
+  int t0 = t_beg + 16 * w;
+  if (t0 < t_end) load(B0, ks0, t0);
+
   // per-head int8 query, one wave per head row; rows past the group are zero
   for (int hl = w; hl < 16; hl += 4) {
     const int h = g * grp + hl;
@@ -154,24 +176,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
 #pragma unroll
   for (int kk = 0; kk < KS; kk++)
     A[kk] = *(const v4i*)(qq + (lane & 15) * QROW + 64 * kk + 16 * (lane >> 4));
-  const int kvd = a.kvh * HD;
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(G.kc, (uint32_t)((size_t)G.k_len * kvd));
-  const int t_end = min(t_beg + a.p1_chunk, G.en);
-  float* srow = a.sc + (size_t)r * a.nh * a.sc_stride;
-  for (int t0 = t_beg + 16 * w; t0 < t_end; t0 += 64) {
-    const int t = t0 + (lane & 15);
-    const bool ok = t < t_end;
-    const int slot = G.ring ? t % G.ring : t;
-    const uint32_t base = ok ? (uint32_t)slot * (uint32_t)kvd + (uint32_t)(g * HD + 16 * (lane >> 4)) : FGM_OOB;
-    v4i B[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; kk++) B[kk] = buf_load_b128(rk, base, 64 * kk);
+  auto tile = [&](const v4i* B, float kscale, int t0) {
     v4i acc = {0, 0, 0, 0};
 #pragma unroll
     for (int kk = 0; kk < KS; kk++) acc = mfma16(A[kk], B[kk], acc);
     // D: lane, register i -> head row 4 (lane / 16) + i, position t
-    if (ok) {
-      const float kscale = G.ks[slot];
+    const int t = t0 + (lane & 15);
+    if (t < t_end) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int hl = 4 * (lane >> 4) + i, h = g * grp + hl;
@@ -179,6 +190,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
           srow[(size_t)h * a.sc_stride + (t - G.st)] = ((float)acc[i] * qsc[hl]) * kscale;
       }
     }
+  };
+  for (; t0 < t_end; t0 += 128) {
+    if (t0 + 64 < t_end) load(B1, ks1, t0 + 64);
+    tile(B0, ks0, t0);
+    if (t0 + 64 >= t_end) break;
+    if (t0 + 128 < t_end) load(B0, ks0, t0 + 128);
+    tile(B1, ks1, t0 + 64);
   }
 }
 
@@ -200,12 +218,24 @@ __global__ __launch_bounds__(1024) void attn_softmax_kernel(const AttnArgs a) {
   float* red = lds + 16 * S;
   const float* scr = a.sc + ((size_t)r * a.nh + h) * a.sc_stride;
 
+  // raw scores into LDS (eight loads in flight per thread), and their maximum
   float mx = -INFINITY;
-  for (int u = tid; u < n; u += T) mx = __builtin_fmaxf(mx, scr[u]);
+  for (int b = tid; b < n; b += 8 * T) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = b + j * T < n ? scr[b + j * T] : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int u = b + j * T;
+      if (u < n) lds[(u & 15) * S + (u >> 4)] = v[j];
+      mx = __builtin_fmaxf(mx, v[j]);
+    }
+  }
   mx = block_max(mx, red);
   for (int u = tid; u < n; u += T) {
-    const float x = scr[u] - mx;
-    lds[(u & 15) * S + (u >> 4)] = u < n16 ? exp16(x) : (float)exp((double)x);
+    float* p = lds + (u & 15) * S + (u >> 4);
+    const float x = *p - mx;
+    *p = u < n16 ? exp16(x) : (float)exp((double)x);
   }
   __syncthreads();
   if (tid < 16) {
@@ -257,10 +287,25 @@ __global__ __launch_bounds__(1024) void attn_softmax_kernel(const AttnArgs a) {
   __syncthreads();
   const float inv = red[nw];
 
+  // weights (e * inv) * vs in place of the exponentials, and their maximum
   float wm = 0.0f;
-  for (int u = tid; u < n; u += T) {
-    const int t = G.st + u, slot = G.ring ? t % G.ring : t;
-    wm = __builtin_fmaxf(wm, (lds[(u & 15) * S + (u >> 4)] * inv) * G.vs[slot]);
+  for (int b = tid; b < n; b += 8 * T) {
+    float vsv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int u = b + j * T, t = G.st + u;
+      vsv[j] = u < n ? G.vs[G.ring ? t % G.ring : t] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int u = b + j * T;
+      if (u < n) {
+        float* p = lds + (u & 15) * S + (u >> 4);
+        const float wt = (*p * inv) * vsv[j];
+        *p = wt;
+        wm = __builtin_fmaxf(wm, wt);
+      }
+    }
   }
   wm = block_max(wm, red);
   const bool pos = wm > 0.0f;
@@ -287,7 +332,7 @@ __global__ __launch_bounds__(1024) void attn_softmax_kernel(const AttnArgs a) {
         }
         if (ok) {
           const int u = t - G.st;
-          const float wt = (lds[(u & 15) * S + (u >> 4)] * inv) * G.vs[s];
+          const float wt = lds[(u & 15) * S + (u >> 4)];
           int q = (int)__builtin_fmaf(wt, wq_inv, 0.5f);
           q = q > 65535 ? 65535 : (q < 0 ? 0 : q);
           W = mult * q;
@@ -302,62 +347,74 @@ __global__ __launch_bounds__(1024) void attn_softmax_kernel(const AttnArgs a) {
     *(uint32_t*)(p + 16 * grp) = pb;
     *(uint32_t*)(p + 32 * grp) = pc;
   }
-  int32_t* acc = a.acc + ((size_t)r * a.nh + h) * a.hd;
-  for (int i = tid; i < a.hd; i += T) acc[i] = 0;
-  if (tid == 0) {
-    a.wq[r * a.nh + h] = pos ? wm / 65535.0f : 0.0f;
-    if (h == max(a.h0, g * grp)) a.cnt[r * a.kvh + g] = 0;
-  }
+  if (tid == 0) a.wq[r * a.nh + h] = pos ? wm / 65535.0f : 0.0f;
 }
 
 // ------------------------------------------------------------------ 3. P.V
 // grid (p3_chunks, hd / 64, m * kvh), 256 threads: workgroup (x, y) takes the
-// slots [dom_lo + 256 x, + 256) and dims [64 y, + 64); wave w one 64-slot
-// step, all four 16-dim tiles, all three planes.
+// 64-slot steps [4 spw x, 4 spw (x + 1)) of the row's domain and the dims
+// [64 y, + 64); wave w the steps 4 spw x + 4 s + w, all four 16-dim tiles and
+// all three planes, the next step's operands in flight while one multiplies.
 __global__ __launch_bounds__(256) void attn_pv_kernel(const AttnArgs a) {
   __shared__ int32_t red[4][16][64];
-  __shared__ int last;
   const int r = blockIdx.z / a.kvh, g = blockIdx.z - r * a.kvh;
   const Geo G = row_geo(a, r);
   const int grp = a.nh / a.kvh;
   const int hb = max(a.h0, g * grp), he = min(a.h1, (g + 1) * grp);
   if (hb >= he) return;
-  const int nchunk = max(1, (G.dom_steps + 3) >> 2);
+  const int spw = a.p3_spw;
+  const int nchunk = max(1, (G.dom_steps + 4 * spw - 1) / (4 * spw));
   if ((int)blockIdx.x >= nchunk) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int kvd = a.kvh * a.hd, d0 = 64 * blockIdx.y;
-  const int step = (int)blockIdx.x * 4 + w;
+  const int hl = lane & 15, q4 = lane >> 4;
+  const int h = g * grp + hl;
+  const bool live = hl < grp && h >= hb && h < he;
+  const int ngroups = (G.k_len + 3) >> 2;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(G.vc, (uint32_t)((size_t)ngroups * kvd * 4));
+  const int8_t* wrow = a.wpl + (size_t)(r * a.kvh + g) * a.wpl_blocks * (48 * grp) + hl * 16;
   v4i D[3][4];
 #pragma unroll
   for (int p = 0; p < 3; p++)
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) D[p][nt] = v4i{0, 0, 0, 0};
-  if (step < G.dom_steps) {
+  // A: plane p, row hl, the 16 slots s0 + 16 q4 + [0, 16); B: dim
+  // d0 + 16 nt + hl, dword q = the four slots of group s0 / 4 + 4 q4 + q
+  auto load = [&](v4i* A, int* B, int step) {
     const int s0 = G.dom_lo + 64 * step;
-    const int hl = lane & 15, q4 = lane >> 4;
-    const int h = g * grp + hl;
-    const bool live = hl < grp && h >= hb && h < he;
-    // A: plane p, row hl, the 16 slots s0 + 16 q4 + [0, 16)
-    const int8_t* wp = a.wpl + ((size_t)(r * a.kvh + g) * a.wpl_blocks + ((s0 - G.dom_lo) >> 4) + q4) *
-                                   (48 * grp) + hl * 16;
-    v4i A[3];
+    const int8_t* wp = wrow + (size_t)(((s0 - G.dom_lo) >> 4) + q4) * (48 * grp);
 #pragma unroll
     for (int p = 0; p < 3; p++) A[p] = live ? *(const v4i*)(wp + p * 16 * grp) : v4i{0, 0, 0, 0};
-    // B: dim d0 + 16 nt + hl; dword q = the four slots of group s0 / 4 + 4 q4 + q
-    const int ngroups = (G.k_len + 3) >> 2;
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(G.vc, (uint32_t)((size_t)ngroups * kvd * 4));
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
-      const int j = g * a.hd + d0 + 16 * nt + hl;
-      v4i B;
+      const uint32_t j = (uint32_t)(g * a.hd + d0 + 16 * nt + hl);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int gi = (s0 >> 2) + 4 * q4 + q;
-        B[q] = buf_load_b32(rv, gi < ngroups ? ((uint32_t)gi * (uint32_t)kvd + (uint32_t)j) * 4u : FGM_OOB, 0);
+        B[4 * nt + q] = buf_load_b32(rv, gi < ngroups ? ((uint32_t)gi * (uint32_t)kvd + j) * 4u : FGM_OOB, 0);
       }
-#pragma unroll
-      for (int p = 0; p < 3; p++) D[p][nt] = mfma16(A[p], B, D[p][nt]);
     }
+  };
+  auto mul = [&](const v4i* A, const int* B) {
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const v4i b = {B[4 * nt], B[4 * nt + 1], B[4 * nt + 2], B[4 * nt + 3]};
+#pragma unroll
+      for (int p = 0; p < 3; p++) D[p][nt] = mfma16(A[p], b, D[p][nt]);
+    }
+  };
+  const int first = (int)blockIdx.x * 4 * spw;
+  const int last = min(first + 4 * spw, G.dom_steps);
+  v4i A0[3], A1[3];
+  int B0[16], B1[16];
+  int step = first + w;
+  if (step < last) load(A0, B0, step);
+  for (; step < last; step += 8) {
+    if (step + 4 < last) load(A1, B1, step + 4);
+    mul(A0, B0);
+    if (step + 4 >= last) break;
+    if (step + 8 < last) load(A0, B0, step + 8);
+    mul(A1, B1);
   }
   // sum iw v = a 2^14 + b 2^7 + c (modulo 2^32, as the reference's int32 lanes)
 #pragma unroll
@@ -367,29 +424,34 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(const AttnArgs a) {
       red[w][4 * (lane >> 4) + i][16 * nt + (lane & 15)] =
           (int32_t)(((uint32_t)D[0][nt][i] << 14) + ((uint32_t)D[1][nt][i] << 7) + (uint32_t)D[2][nt][i]);
   __syncthreads();
-  for (int idx = tid; idx < 16 * 64; idx += 256) {
-    const int hl = idx >> 6, d = idx & 63, h = g * grp + hl;
-    if (hl < grp && h >= hb && h < he) {
-      const uint32_t s = (uint32_t)red[0][hl][d] + (uint32_t)red[1][hl][d] + (uint32_t)red[2][hl][d] +
-                         (uint32_t)red[3][hl][d];
-      if (s) atomicAdd(a.acc + ((size_t)r * a.nh + h) * a.hd + d0 + d, (int)s);
-    }
+  int32_t* part = a.part + ((size_t)(r * a.kvh + g) * a.p3_chunks + blockIdx.x) * grp * a.hd + d0;
+  for (int idx = tid; idx < grp * 64; idx += 256) {
+    const int hr = idx >> 6, d = idx & 63;
+    part[(size_t)hr * a.hd + d] = (int32_t)((uint32_t)red[0][hr][d] + (uint32_t)red[1][hr][d] +
+                                            (uint32_t)red[2][hr][d] + (uint32_t)red[3][hr][d]);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t total = (uint32_t)nchunk * (uint32_t)(a.hd >> 6);
-    last = atomicAdd(a.cnt + r * a.kvh + g, 1u) == total - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int idx = tid; idx < (he - hb) * a.hd; idx += 256) {
-    const int h = hb + idx / a.hd, i = idx - (h - hb) * a.hd;
-    const size_t o = ((size_t)r * a.nh + h) * a.hd + i;
-    const int v = __hip_atomic_load(a.acc + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    a.out[o] = (float)v * a.wq[r * a.nh + h];
-  }
+}
+
+// ---------------------------------------------------------------- 4. final
+// grid (m * (h1 - h0), hd / 64), 64 threads: one dim per thread, all of the
+// row's chunk partials in flight at once (at most 32); out = (float)(their
+// sum) * (wmax / 65535), 0 when the weights were all zero.
+__global__ __launch_bounds__(64) void attn_final_kernel(const AttnArgs a) {
+  const int nhr = a.h1 - a.h0;
+  const int r = blockIdx.x / nhr, h = a.h0 + ((int)blockIdx.x - r * nhr);
+  const int grp = a.nh / a.kvh, g = h / grp, hl = h - g * grp;
+  const Geo G = row_geo(a, r);
+  const int nchunk = max(1, (G.dom_steps + 4 * a.p3_spw - 1) / (4 * a.p3_spw));
+  const int i = 64 * blockIdx.y + threadIdx.x;
+  const int32_t* part = a.part + (size_t)(r * a.kvh + g) * a.p3_chunks * grp * a.hd + (size_t)hl * a.hd + i;
+  const size_t cs = (size_t)grp * a.hd;
+  uint32_t v[32];
+#pragma unroll
+  for (int c = 0; c < 32; c++) v[c] = c < nchunk ? (uint32_t)part[c * cs] : 0u;
+  uint32_t t = 0;  // integer sum: any order gives the same bits
+#pragma unroll
+  for (int c = 0; c < 32; c++) t += v[c];
+  a.out[((size_t)r * a.nh + h) * a.hd + i] = (float)(int32_t)t * a.wq[r * a.nh + h];
 }
 
 // ----------------------------------------------------------- cache writes
@@ -457,27 +519,26 @@ size_t fgm_attn_layout(AttnArgs* a, void* base, int m, int nh, int kvh, int hd, 
   const int sc_stride = (max_span + 63) / 64 * 64;
   // a domain spans at most max_span + 3 slots from a 64-aligned start
   const int wpl_blocks = ((max_span + 3 + 63) / 64 + 1) * 4;
+  const int chunks = attn_pv_chunks(m, kvh, hd);
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   size_t off = 0;
   const size_t o_sc = off;
   off = al(off + (size_t)m * nh * sc_stride * 4);
   const size_t o_wpl = off;
   off = al(off + (size_t)m * kvh * wpl_blocks * 48 * grp);
-  const size_t o_acc = off;
-  off = al(off + (size_t)m * nh * hd * 4);
+  const size_t o_part = off;
+  off = al(off + (size_t)m * kvh * chunks * grp * hd * 4);
   const size_t o_wq = off;
   off = al(off + (size_t)m * nh * 4);
-  const size_t o_cnt = off;
-  off = al(off + (size_t)m * kvh * 4);
   if (a && base) {
     char* b = (char*)base;
     a->sc = (float*)(b + o_sc);
     a->sc_stride = sc_stride;
     a->wpl = (int8_t*)(b + o_wpl);
     a->wpl_blocks = wpl_blocks;
-    a->acc = (int32_t*)(b + o_acc);
+    a->part = (int32_t*)(b + o_part);
+    a->p3_chunks = chunks;
     a->wq = (float*)(b + o_wq);
-    a->cnt = (uint32_t*)(b + o_cnt);
   }
   return off;
 }
@@ -502,12 +563,17 @@ hipError_t fgm_launch_attn(const AttnArgs& a, int max_n, hipStream_t st) {
   static hipError_t attr = hipFuncSetAttribute((const void*)attn_softmax_kernel,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  const int T = max_n <= 2048 ? 256 : (max_n <= 8192 ? 512 : 1024);
+  // long rows with few (row, head) pairs get the widest workgroups; with
+  // hundreds of pairs the chip is full anyway
+  const int nwg = a.m * (a.h1 - a.h0);
+  const int T = max_n <= 1024 ? 256 : (max_n >= 4096 && nwg < 256 ? 1024 : 512);
   const int S = (((max_n + 15) >> 4) + 16 + 63) / 64 * 64 + 4;
   const size_t lds = ((size_t)16 * S + 32) * 4;
   hipLaunchKernelGGL(attn_softmax_kernel, dim3(a.m * (a.h1 - a.h0)), dim3(T), lds, st, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(attn_pv_kernel, dim3(a.p3_chunks, a.hd / 64, a.m * a.kvh), dim3(256), 0, st, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_final_kernel, dim3(a.m * (a.h1 - a.h0), a.hd / 64), dim3(64), 0, st, a);
   return hipGetLastError();
 }
 

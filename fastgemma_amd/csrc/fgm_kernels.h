@@ -92,12 +92,12 @@ struct AttnArgs {
   int sc_stride;
   int8_t* wpl;        // weight planes [m][kvh][wpl_blocks][3][grp][16]
   int wpl_blocks;
-  int32_t* acc;       // [m][nh][hd]
+  int32_t* part;      // P.V partial sums [m][kvh][p3_chunks][grp][hd]
   float* wq;          // per (row, head) dequantisation step, 0 = zero output
-  uint32_t* cnt;      // [m][kvh] completion tickets
   int p1_chunk;       // positions per score workgroup
   int p1_chunks;      // score workgroups per (row, kv head) in the grid
-  int p3_chunks;      // slot chunks (256 slots) per (row, kv head) in the grid
+  int p3_spw;         // 64-slot steps per wave in a P.V workgroup
+  int p3_chunks;      // P.V slot chunks (4 * p3_spw steps) per (row, kv head)
 };
 // A row's attended range and the reference's slot runs (ops.c:560-572) as
 // four-slot-aligned spans [lo, hi); the P.V slot domain is
@@ -129,6 +129,12 @@ __host__ __device__ inline AttnSpan attn_span(int en, int lo, int window, int ri
   g.dom_lo = (g.nrun == 2 ? 0 : g.lo0) & ~63;
   g.dom_steps = (g.hi0 - g.dom_lo + 63) >> 6;
   return g;
+}
+// P.V slot chunks per (row, kv head): enough workgroups to fill the chip
+// (about 2048), at most 32.
+inline int attn_pv_chunks(int m, int kvh, int hd) {
+  const int per = (2048 + m * kvh * (hd / 64) - 1) / (m * kvh * (hd / 64));
+  return per < 1 ? 1 : (per > 32 ? 32 : per);
 }
 // scratch layout for `m` rows whose spans (max over rows of end - start and
 // of the ring size) are at most max_span; returns the bytes and fills the
