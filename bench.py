@@ -459,6 +459,79 @@ def extra_attn(gpu):
     return {"workload": "attention per layer call, graphs of 8 calls", "per_case": res}
 
 
+def extra_model(gpu):
+    """A .fgm file on the GPU (model.rs, forward.rs:26-158): a synthetic file
+    with the cfg2 up / down shapes (int4 g64, Hadamard 128) and an int8 twin
+    of up, opened resident (one upload), Gemm::run (FWHT + quantise + pack,
+    then the GEMM) through the DualW rule FGM_WEIGHTS=auto:16 at M=8 (int4)
+    and M=256 (the int8 twin), against the host-pointer drop-ins on the same
+    bytes (per call: activation up, result down; weights cached)."""
+    import tempfile
+    import numpy as np
+    from fastgemma_amd import kernels
+    from fastgemma_amd.fgm_format import write_fgm
+    from fastgemma_amd.model import Model, Selection, linear_run
+    t = gpu.t
+    rng = np.random.default_rng(7)
+    tensors = []
+    for name, n, k, twin in (("up", 8192, 2048, True), ("down", 2048, 8192, False)):
+        tensors.append((name, rng.integers(0, 256, n * k // 2, dtype=np.uint8), "q4g", (n, k),
+                        {"hadamard": 128, "group": 64}))
+        tensors.append((name + ".scale", (rng.random((k // 64) * n) * 0.045 + 0.005).astype(np.float16),
+                        "f16", (k // 64, n), None))
+        if twin:
+            tensors.append((name + ".i8", rng.integers(-127, 128, n * k, dtype=np.int8), "q8c", (n, k),
+                            {"hadamard": 128, "group": 0}))
+            tensors.append((name + ".i8.scale", (rng.random(n) * 0.009 + 0.001).astype(np.float32), "f32",
+                            (n,), None))
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = d + "/bench.fgm"
+        write_fgm(path, {"hidden_size": 2048}, tensors)
+        t0 = time.perf_counter()
+        m = Model(path, resident=True)
+        t.cuda.synchronize()
+        open_s = time.perf_counter() - t0
+        res["open_resident"] = {"s": open_s, "bytes": m.total_bytes(),
+                                "GB_s": m.total_bytes() / open_s / 1e9}
+        sel = Selection.parse("auto:16")
+        for rows in (8, 256):
+            w = m.dual("up").pick(rows, sel)
+            a = t.randn(rows, w.k, device=gpu.dev)
+            out = t.empty(rows, w.n, device=gpu.dev)
+            scratch = t.empty(max(kernels.lib().fgm_hip_linear_scratch_bytes(rows, w.k), 1),
+                              dtype=t.uint8, device=gpu.dev)
+            dt = kernel_avg(gpu, lambda i: linear_run(w, a, rows, w.k, out, scratch), 16, 3)
+            wb = w.n * w.k // 2 if w.bits == 4 else w.n * w.k
+            res[f"linear_run up M={rows}"] = {"bits": w.bits, "us": dt * 1e6,
+                                              "GB_s_weights": wb / dt / 1e9,
+                                              "TOPS": 2.0 * rows * w.n * w.k / dt / 1e12}
+            # the drop-in path on the same bytes (host activation and result)
+            ah = a.cpu().numpy()
+            qs = np.empty(rows, np.float32)
+            pa = np.empty(kernels.packed_a_len(rows, w.k), np.int8)
+            rot = np.empty(rows * w.k, np.float32)
+            qa = np.empty(rows * w.k, np.int8)
+            c = np.empty(rows * w.n, np.float32)
+            blob, scl = np.ascontiguousarray(w.blob()), np.ascontiguousarray(w.scales())
+
+            def dropin():
+                kernels.prep_rows(ah.ravel(), w.k, rot, qa, qs, pa, rows, w.k, w.hadamard, 0, rows)
+                if w.bits == 4:
+                    kernels.gemm_q4g(rows, w.n, w.k, pa, qs, blob, scl, w.group, c, w.n, 0, w.n // 16)
+                else:
+                    kernels.gemm_q8c(rows, w.n, w.k, pa, qs, blob, scl, c, w.n, 0, w.n // 16)
+            dropin()
+            reps = 20
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                dropin()
+            res[f"dropin up M={rows}"] = {"bits": w.bits, "us": (time.perf_counter() - t0) / reps * 1e6}
+        m.close()
+    return {"workload": "synthetic .fgm (cfg2 up/down int4 + int8 twin of up), resident vs drop-in",
+            "per_case": res}
+
+
 # ------------------------------------------------------------ CPU baseline
 def cpu_baseline(host, budget_s=10.0):
     import numpy as np
@@ -546,7 +619,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
                     help="run one extra measurement (cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
-                         "attn) and print its JSON instead of the headline line")
+                         "attn, model) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -557,7 +630,8 @@ def main():
     gpu = Gpu()
     gpu.t.manual_seed(1234)
     extras = {"cfg1": extra_cfg1, "int4_stream": extra_int4_stream, "cfg3": extra_cfg3,
-              "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem, "attn": extra_attn}
+              "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem, "attn": extra_attn,
+              "model": extra_model}
     if args.only is not None:
         if args.only not in extras:
             print(f"--only: unknown measurement {args.only!r} (one of {', '.join(extras)})",

@@ -36,6 +36,14 @@ def lib() -> _C.CDLL:
             raise HipUnavailable(
                 f"{LIB_PATH} is missing: build it with `make -C fastgemma_amd/csrc` "
                 "or __graft_entry__.build()")
+        # torch (the test and benchmark plumbing) ships its own HIP runtime
+        # under the same soname as the system one this library links; the
+        # first one loaded serves the whole process, and torch only
+        # initialises the GPU through its own.  Load it first when present.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = _C.CDLL(LIB_PATH)
         _bind(L)
         _LIB = L
@@ -97,6 +105,38 @@ def _bind(L: _C.CDLL) -> None:
                                            _C.c_size_t, p]
     L.fgm_hip_store_v_t_dev.argtypes = [p, p, i, i, p]
     L.fgm_hip_kv_store_dev.argtypes = [p, p, i, i, p, p, p, p, i, i, i, p]
+    L.fgm_hip_model_open.argtypes = [_C.c_char_p, i]
+    L.fgm_hip_model_open.restype = p
+    L.fgm_hip_model_close.argtypes = [p]
+    L.fgm_hip_model_close.restype = None
+    L.fgm_hip_model_has.argtypes = [p, _C.c_char_p]
+    L.fgm_hip_model_config.argtypes = [p]
+    L.fgm_hip_model_config.restype = _C.c_char_p
+    L.fgm_hip_model_meta.argtypes = [p]
+    L.fgm_hip_model_meta.restype = _C.c_char_p
+    L.fgm_hip_model_total_bytes.argtypes = [p]
+    L.fgm_hip_model_total_bytes.restype = _C.c_size_t
+    L.fgm_hip_model_tensor_count.argtypes = [p]
+    L.fgm_hip_model_tensor_name.argtypes = [p, i]
+    L.fgm_hip_model_tensor_name.restype = _C.c_char_p
+    L.fgm_hip_model_tensor.argtypes = [p, _C.c_char_p, p]
+    L.fgm_hip_model_linear.argtypes = [p, _C.c_char_p, p]
+    L.fgm_hip_weight_sel.argtypes = [_C.c_char_p, p]
+    L.fgm_hip_model_dual.argtypes = [p, _C.c_char_p, i, i, i, p]
+    L.fgm_hip_model_gather_dev.argtypes = [p, _C.c_char_p, p, i, p, p]
+    L.fgm_hip_gather_dev.argtypes = [i, p, p, p, i, i, p, p]
+    L.fgm_gather_q8r_hip.argtypes = [p, p, p, i, i]
+    L.fgm_gather_q4r_hip.argtypes = [p, p, p, i, i]
+    L.fgm_hip_pool_gemm_dev.argtypes = [p, p]
+    L.fgm_hip_pool_prep_dev.argtypes = [p, p]
+    L.fgm_hip_linear_scratch_bytes.argtypes = [i, i]
+    L.fgm_hip_linear_scratch_bytes.restype = _C.c_size_t
+    L.fgm_hip_linear_run_dev.argtypes = [p, p, i, i, p, p, _C.c_size_t, p]
+    for name in ("fgm_hip_model_has", "fgm_hip_model_tensor_count", "fgm_hip_model_tensor",
+                 "fgm_hip_model_linear", "fgm_hip_weight_sel", "fgm_hip_model_dual",
+                 "fgm_hip_model_gather_dev", "fgm_hip_gather_dev", "fgm_hip_pool_gemm_dev",
+                 "fgm_hip_pool_prep_dev", "fgm_hip_linear_run_dev"):
+        getattr(L, name).restype = i
     for name in ("fgm_hip_attend_dev", "fgm_hip_attend_heads_dev", "fgm_hip_store_v_t_dev",
                  "fgm_hip_kv_store_dev", "fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
@@ -126,6 +166,35 @@ class PrepDesc(_C.Structure):
                 ("qa", _C.c_void_p), ("qs", _C.c_void_p), ("pa", _C.c_void_p),
                 ("m", _C.c_int), ("k", _C.c_int), ("hsz", _C.c_int), ("r0", _C.c_int),
                 ("r1", _C.c_int)]
+
+
+class TensorInfo(_C.Structure):
+    """fgm_hip_tensor (include/fgm_hip.h)."""
+    _fields_ = [("dtype", _C.c_char * 16), ("ndim", _C.c_int), ("shape", _C.c_int64 * 4),
+                ("offset", _C.c_size_t), ("nbytes", _C.c_size_t), ("host", _C.c_void_p),
+                ("dev", _C.c_void_p), ("hadamard", _C.c_int), ("group", _C.c_int)]
+
+
+class LinearInfo(_C.Structure):
+    """fgm_hip_linear (include/fgm_hip.h)."""
+    _fields_ = [("bits", _C.c_int), ("n", _C.c_int), ("k", _C.c_int), ("group", _C.c_int),
+                ("hadamard", _C.c_int), ("b", _C.c_void_p), ("b_scale", _C.c_void_p),
+                ("b_host", _C.c_void_p), ("b_scale_host", _C.c_void_p)]
+
+
+class GemmJob(_C.Structure):
+    """fgm_hip_gemm_job (include/fgm_hip.h; pool.rs:19-34)."""
+    _fields_ = [("m", _C.c_int), ("n", _C.c_int), ("kdim", _C.c_int), ("a", _C.c_void_p),
+                ("a_scale", _C.c_void_p), ("bq", _C.c_void_p), ("b8", _C.c_void_p),
+                ("s4", _C.c_void_p), ("s8", _C.c_void_p), ("bits", _C.c_int),
+                ("group", _C.c_int), ("c", _C.c_void_p), ("ldc", _C.c_int)]
+
+
+class PrepJob(_C.Structure):
+    """fgm_hip_prep_job (include/fgm_hip.h; pool.rs:67-79)."""
+    _fields_ = [("src", _C.c_void_p), ("lda", _C.c_int), ("rot", _C.c_void_p),
+                ("qa", _C.c_void_p), ("qs", _C.c_void_p), ("pa", _C.c_void_p), ("m", _C.c_int),
+                ("k", _C.c_int), ("hsz", _C.c_int)]
 
 
 class AttnSeq(_C.Structure):

@@ -314,6 +314,11 @@ int check_prep(const fgm_hip_prep_desc& d) {
 }  // namespace
 
 // ====================================================================== C ABI
+// Status helpers for the library's other sources (fgm_model.hip).
+int fgm_status_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+int fgm_status_hip(hipError_t e, const char* what) { return hip_fail(e, what); }
+int fgm_status_device() { return ensure_device(); }
+
 extern "C" {
 
 const char* fgm_hip_last_error(void) { return g_err; }

@@ -228,6 +228,100 @@ int fgm_hip_store_v_t_dev(int8_t *vt, const int8_t *src, int n, int slot, void *
 int fgm_hip_kv_store_dev(const float *k, const float *v, int m, int row_len, int8_t *kc, float *ks,
                          int8_t *vt, float *vs, int cap, int pos, int ring, void *stream);
 
+/* ------------------------------------------------------------- the model
+ * A .fgm file (convert/fgm.py:1-16; model.rs:1-220) opened on the GPU: the file
+ * is mapped read-only and, with device_resident, its tensor body is copied to
+ * HBM once, so GEMMs read weights with no host traffic.  Tensor pointers stay
+ * valid until fgm_hip_model_close.  NULL / non-zero status on error, with
+ * fgm_hip_last_error() describing it. */
+typedef struct fgm_hip_model fgm_hip_model;
+
+typedef struct fgm_hip_tensor {
+  char dtype[16];          /* q4g, q8c, q8r, q4r, f32, f16, ... */
+  int ndim;
+  int64_t shape[4];
+  size_t offset, nbytes;   /* in the file */
+  const void *host;        /* in the mapping */
+  const void *dev;         /* in HBM, NULL unless resident */
+  int hadamard;            /* meta.hadamard, 0 when absent */
+  int group;               /* meta.group, -1 when absent */
+} fgm_hip_tensor;
+
+/* A quantised linear weight (model.rs:104-117, QLinear): bits 4 (q4g: b packed
+ * int4, b_scale f16 [k/group][n]) or 8 (q8c: b int8 tiles, b_scale f32 [n]). */
+typedef struct fgm_hip_linear {
+  int bits, n, k, group, hadamard;
+  const void *b, *b_scale;            /* device (NULL unless resident) */
+  const void *b_host, *b_scale_host;  /* in the mapping */
+} fgm_hip_linear;
+
+fgm_hip_model *fgm_hip_model_open(const char *path, int device_resident);  /* Model::open, model.rs:120-128 */
+void fgm_hip_model_close(fgm_hip_model *m);
+int fgm_hip_model_has(const fgm_hip_model *m, const char *name);           /* model.rs:130-132 */
+const char *fgm_hip_model_config(const fgm_hip_model *m);                  /* header "config", compact JSON */
+const char *fgm_hip_model_meta(const fgm_hip_model *m);                    /* header "meta" */
+size_t fgm_hip_model_total_bytes(const fgm_hip_model *m);                  /* model.rs:209-211 */
+int fgm_hip_model_tensor_count(const fgm_hip_model *m);
+const char *fgm_hip_model_tensor_name(const fgm_hip_model *m, int i);      /* sorted by name */
+int fgm_hip_model_tensor(const fgm_hip_model *m, const char *name, fgm_hip_tensor *out);
+int fgm_hip_model_linear(const fgm_hip_model *m, const char *name, fgm_hip_linear *out); /* model.rs:167-192 */
+
+/* The int4 / int8 weight choice (forward.rs:26-89).  FGM_WEIGHTS = int4 -> LO,
+ * int8 -> HI, auto:M -> ABOVE M (M not a number: 16), anything else or unset
+ * -> ABOVE 16.  fgm_hip_model_dual resolves <name> or its int8 twin
+ * <name>.i8 (model.rs:194-201, DualW::pick): the twin when it exists and sel
+ * is HI, or ABOVE with rows >= threshold. */
+#define FGM_HIP_SEL_LO 0
+#define FGM_HIP_SEL_HI 1
+#define FGM_HIP_SEL_ABOVE 2
+int fgm_hip_weight_sel(const char *value, int *threshold);
+int fgm_hip_model_dual(const fgm_hip_model *m, const char *name, int rows, int sel, int threshold,
+                       fgm_hip_linear *out);
+
+/* Embedding / PLE gathers (model.rs:203-213; ops.c:208-251): out[r][0..k) =
+ * row rows[r] of a q8r (int8, f32 scale per row) or q4r (int4 half-split
+ * nibbles, f16 scale per 64) table; exact products. */
+void fgm_gather_q8r_hip(float *out, const int8_t *tbl, const float *sc, int row, int k); /* lib.rs:54, ops.c:208-217 */
+void fgm_gather_q4r_hip(float *out, const uint8_t *tbl, const uint16_t *sc, int row, int k); /* lib.rs:55, ops.c:228-251 */
+int fgm_hip_gather_dev(int bits, const void *tbl, const void *sc, const int *rows, int count, int k,
+                       float *out, void *stream);
+int fgm_hip_model_gather_dev(const fgm_hip_model *m, const char *name, const int *rows, int count,
+                             float *out, void *stream);
+
+/* The thread pool's jobs on the HIP backend (pool.rs:19-79, 285-310): one
+ * launch covers all of N (GEMM) or all tile blocks (prep) instead of a split
+ * over host threads.  Device pointers. */
+typedef struct fgm_hip_gemm_job {
+  int m, n, kdim;
+  const int8_t *a;
+  const float *a_scale;
+  const uint8_t *bq;
+  const int8_t *b8;
+  const uint16_t *s4;
+  const float *s8;
+  int bits, group;
+  float *c;
+  int ldc;
+} fgm_hip_gemm_job;
+typedef struct fgm_hip_prep_job {
+  const float *src;
+  int lda;
+  float *rot;
+  int8_t *qa;
+  float *qs;
+  int8_t *pa;
+  int m, k, hsz;
+} fgm_hip_prep_job;
+int fgm_hip_pool_gemm_dev(const fgm_hip_gemm_job *job, void *stream);
+int fgm_hip_pool_prep_dev(const fgm_hip_prep_job *job, void *stream);
+
+/* Gemm::run (forward.rs:140-158): out[m][0..n) = w . a[m][0..k) -- FWHT of
+ * w.hadamard, per-row quantisation and tile packing into `scratch` (at least
+ * fgm_hip_linear_scratch_bytes(m, k) bytes), then the GEMM. */
+size_t fgm_hip_linear_scratch_bytes(int m, int k);
+int fgm_hip_linear_run_dev(const fgm_hip_linear *w, const float *a, int m, int lda, float *out,
+                           void *scratch, size_t scratch_bytes, void *stream);
+
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);

@@ -91,6 +91,8 @@ def lib() -> C.CDLL:
         L.orc_attend_q8_row.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i]
         L.orc_store_v_t.argtypes = [_p, _p, _i, _i]
         L.orc_rowbatch_scratch.restype = _i
+        L.orc_gather_q8r.argtypes = [_p, _p, _p, _i, _i]
+        L.orc_gather_q4r.argtypes = [_p, _p, _p, _i, _i]
         L.orc_rowbatch_scratch.argtypes = [_i, _i, _i]
         L.orc_xorshift_fill.restype = _u64
         L.orc_xorshift_fill.argtypes = [_u64, _sz, _i, _i, _p]
@@ -130,6 +132,8 @@ def _bind_ref(L: C.CDLL) -> None:
     L.fgm_attend_q8_row.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i, _i]
     L.fgm_store_v_t.argtypes = [_p, _p, _i, _i]
     L.fgm_rowbatch_scratch.restype = _i
+    L.fgm_gather_q8r.argtypes = [_p, _p, _p, _i, _i]
+    L.fgm_gather_q4r.argtypes = [_p, _p, _p, _i, _i]
     L.fgm_rowbatch_scratch.argtypes = [_i, _i, _i]
 
 
@@ -488,4 +492,23 @@ def ref_attend(kind: str, q, kv: KvLayer, n_heads: int, start: int, end: int, h0
         R.fgm_attend_q8_heads(*args, h0, h1, ring, kv.cap)
     else:
         R.fgm_attend_q8_row(*args, ring, kv.cap)
+    return out
+
+
+# ---------------------------------------------------------- gather tables
+def gather(bits: int, tbl: np.ndarray, sc: np.ndarray, row: int, k: int) -> np.ndarray:
+    """fgm_gather_q8r / fgm_gather_q4r (ops.c:208-251)."""
+    out = np.empty(k, np.float32)
+    f = lib().orc_gather_q8r if bits == 8 else lib().orc_gather_q4r
+    f(_ptr(out), _ptr(tbl), _ptr(sc), row, k)
+    return out
+
+
+def ref_gather(bits: int, tbl: np.ndarray, sc: np.ndarray, row: int, k: int):
+    R = ref()
+    if R is None:
+        return None
+    out = np.empty(k, np.float32)
+    f = R.fgm_gather_q8r if bits == 8 else R.fgm_gather_q4r
+    f(_ptr(out), _ptr(tbl), _ptr(sc), row, k)
     return out

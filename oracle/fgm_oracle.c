@@ -736,3 +736,25 @@ void orc_store_v_t(int8_t *vt, const int8_t *src, int n, int slot) {
 int orc_rowbatch_scratch(int n_heads, int cap, int head_dim) {
   return n_heads * cap + (cap + 3) / 2 + 2 * head_dim + 64;
 }
+
+/* fgm_gather_q8r (ops.c:208-217): out = (float)q * sc[row] */
+void orc_gather_q8r(float *out, const int8_t *tbl, const float *sc, int row, int k) {
+  const int8_t *p = tbl + (size_t)row * k;
+  for (int i = 0; i < k; i++) out[i] = (float)p[i] * sc[row];
+}
+
+/* fgm_gather_q4r (ops.c:228-251): per 64-block, 32 packed bytes; element j <
+ * 32 is the low nibble of byte j, element j >= 32 the high nibble of byte
+ * j - 32 (two's complement); scale f16 [row][k/64] widened exactly. */
+void orc_gather_q4r(float *out, const uint8_t *tbl, const uint16_t *sc, int row, int k) {
+  const int g = k / 64;
+  const uint8_t *p = tbl + (size_t)row * (k / 2);
+  for (int b = 0; b < g; b++) {
+    const float s = orc_f16_to_f32(sc[(size_t)row * g + b]);
+    for (int j = 0; j < 64; j++) {
+      const uint8_t byte = p[b * 32 + (j & 31)];
+      const int nib = j < 32 ? (byte & 15) : (byte >> 4);
+      out[b * 64 + j] = (float)((nib ^ 8) - 8) * s;
+    }
+  }
+}
