@@ -443,8 +443,8 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // deeper ring.
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
-    if (tiles(in, 128, 128) >= 240) return launch_any<8, 2, 2, 2, 2, 3, 2>(in, st);
-    if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 2, 2>(in, st);
+    if (tiles(in, 128, 128) >= 240) return launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
+    if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
     return launch_any<8, 1, 1, 2, 1, 4, 2>(in, st);
   }
   if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
