@@ -2,7 +2,8 @@
 // fgm_attend_q8_row (ops.c:353-877), the transposed V store (ops.c:653-657)
 // and the forward pass's KV append (forward.rs:515-548).
 //
-// One call is four launches:
+// One call is four launches (one for short rows, see the single-launch path
+// below):
 //  1. attn_scores_kernel: s = ((float)(K.q) * qscale) * kscale for every
 //     (row, head, position).  Each workgroup makes the per-head int8 query
 //     (amax, 127 / amax, round to nearest even, clamp +-127; ops.c:417-433);
@@ -28,6 +29,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "fgm_common.h"
 #include "fgm_kernels.h"
@@ -454,6 +456,304 @@ __global__ __launch_bounds__(64) void attn_final_kernel(const AttnArgs a) {
   a.out[((size_t)r * a.nh + h) * a.hd + i] = (float)(int32_t)t * a.wq[r * a.nh + h];
 }
 
+// ------------------------------------------------------ single-launch path
+// Rows of at most FUSED_MAX_N positions and kv groups of at most 8 query
+// heads: one workgroup per (row, kv head) does all four steps above with the
+// same arithmetic, the scores, exponentials and weight planes in LDS and the
+// P.V sums in registers -- one launch instead of four (sliding-window layers,
+// short contexts).  grid (m * kvh), 512 threads; dynamic LDS:
+//   qq [16][hd + 16] int8 | qsc, wqs, winv [16] f32 |
+//   E [grp][16][S] f32 (per head, e[16 c + j] at [j][c]) |
+//   planes [blocks][3][grp][16] int8.
+constexpr int FUSED_MAX_N = 1024, FUSED_MAX_GRP = 8, FUSED_T = 512, FUSED_NW = FUSED_T / 64;
+
+__host__ __device__ inline size_t fused_lds(int hd, int grp, int max_n, int blocks) {
+  const int S = (((max_n + 15) >> 4) + 16 + 63) / 64 * 64 + 4;
+  return (size_t)16 * (hd + 16) + 48 * 4 + (size_t)grp * 16 * S * 4 + (size_t)blocks * 48 * grp;
+}
+
+template <int KS>
+__global__ __launch_bounds__(FUSED_T) void attn_fused_kernel(const AttnArgs a) {
+  constexpr int HD = KS * 64, QROW = HD + 16, NW = FUSED_NW;
+  extern __shared__ __attribute__((aligned(16))) char sm[];
+  const int r = blockIdx.x / a.kvh, g = blockIdx.x - r * a.kvh;
+  const Geo G = row_geo(a, r);
+  const int grp = a.nh / a.kvh;
+  const int hb = max(a.h0, g * grp), he = min(a.h1, (g + 1) * grp);
+  if (hb >= he) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = max(G.n, 0), n16 = n & ~15, S = exp_stride(n);
+  int8_t* qq = (int8_t*)sm;
+  float* qsc = (float*)(sm + 16 * QROW);
+  float* wqs = qsc + 16;   // per head: wmax / 65535, 0 = zero output
+  float* winv = wqs + 16;  // per head: 1 / sum, then 65535 / wmax
+  float* E = winv + 16;
+  int8_t* PL = (int8_t*)(E + (size_t)grp * 16 * S);
+  const int kvd = a.kvh * HD;
+  auto live_head = [&](int hl) { return hl < grp && g * grp + hl >= hb && g * grp + hl < he; };
+
+  // ---- scores: the first tile's K in flight while the query is quantised
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(G.kc, (uint32_t)((size_t)G.k_len * kvd));
+  auto load = [&](v4i* B, float& kscale, int t0) {
+    const int t = t0 + (lane & 15);
+    const int slot = G.ring ? t % G.ring : t;
+    const bool ok = t < G.en;
+    const uint32_t base = ok ? (uint32_t)slot * (uint32_t)kvd + (uint32_t)(g * HD + 16 * (lane >> 4)) : FGM_OOB;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) B[kk] = buf_load_b128(rk, base, 64 * kk);
+    kscale = ok ? G.ks[slot] : 0.0f;
+  };
+  v4i B0[KS], B1[KS];
+  float ks0 = 0.0f, ks1 = 0.0f;
+  int t0 = G.st + 16 * w;
+  if (t0 < G.en) load(B0, ks0, t0);
+  for (int hl = w; hl < 16; hl += NW) {
+    const int h = g * grp + hl;
+    const bool live = live_head(hl);
+    float x[KS];
+    float amax = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      x[kk] = live ? a.q[((size_t)r * a.nh + h) * HD + 64 * kk + lane] : 0.0f;
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(x[kk]));
+    }
+    amax = wave_max(amax);
+    const float qinv = amax > 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      const float v = __builtin_amdgcn_fmed3f(__builtin_rintf(x[kk] * qinv), -127.0f, 127.0f);
+      qq[hl * QROW + 64 * kk + lane] = (int8_t)(int)v;
+    }
+    if (lane == 0) qsc[hl] = amax / 127.0f;
+  }
+  __syncthreads();
+  v4i A[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; kk++)
+    A[kk] = *(const v4i*)(qq + (lane & 15) * QROW + 64 * kk + 16 * (lane >> 4));
+  auto tile = [&](const v4i* B, float kscale, int tt) {
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) acc = mfma16(A[kk], B[kk], acc);
+    const int t = tt + (lane & 15);
+    if (t < G.en) {
+      const int u = t - G.st;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int hl = 4 * (lane >> 4) + i;
+        if (hl < grp) E[(size_t)hl * 16 * S + (u & 15) * S + (u >> 4)] = ((float)acc[i] * qsc[hl]) * kscale;
+      }
+    }
+  };
+  for (; t0 < G.en; t0 += 32 * NW) {
+    if (t0 + 16 * NW < G.en) load(B1, ks1, t0 + 16 * NW);
+    tile(B0, ks0, t0);
+    if (t0 + 16 * NW >= G.en) break;
+    if (t0 + 32 * NW < G.en) load(B0, ks0, t0 + 32 * NW);
+    tile(B1, ks1, t0 + 16 * NW);
+  }
+  // ---- P.V: wave w takes the 16-dim tiles w, w + NW, ...; every slot step,
+  // three planes, sums in registers
+  const int hl = lane & 15, q4 = lane >> 4;
+  const bool alive = live_head(hl);
+  const int ngroups = (G.k_len + 3) >> 2;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(G.vc, (uint32_t)((size_t)ngroups * kvd * 4));
+  constexpr int NTW = (HD / 16 + NW - 1) / NW;  // dim tiles per wave
+  v4i D[3][NTW];
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+#pragma unroll
+    for (int i = 0; i < NTW; i++) D[p][i] = v4i{0, 0, 0, 0};
+  auto loadv = [&](int* B, int step) {
+    const int s0 = G.dom_lo + 64 * step;
+#pragma unroll
+    for (int i = 0; i < NTW; i++) {
+      const int nt = w + NW * i;
+      const uint32_t j = (uint32_t)(g * HD + 16 * nt + hl);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int gi = (s0 >> 2) + 4 * q4 + q;
+        B[4 * i + q] = (nt < HD / 16 && gi < ngroups)
+                           ? buf_load_b32(rv, ((uint32_t)gi * (uint32_t)kvd + j) * 4u, 0)
+                           : 0;
+      }
+    }
+  };
+  // the first two V steps do not depend on the weights: in flight through
+  // the softmax and the plane writes
+  int V0[4 * NTW], V1[4 * NTW];
+  const int steps = G.dom_steps;
+  if (steps > 0) loadv(V0, 0);
+  if (steps > 1) loadv(V1, 1);
+  __syncthreads();
+
+  // ---- softmax: wave hl owns head hl; the maximum and the exponentials
+  float* Eh = E + (size_t)w * 16 * S;
+  const bool mine = w < grp && live_head(w);
+  if (mine) {
+    float mx = -INFINITY;
+    for (int u = lane; u < n; u += 64) mx = __builtin_fmaxf(mx, Eh[(u & 15) * S + (u >> 4)]);
+    mx = wave_max(mx);
+    for (int u = lane; u < n; u += 64) {
+      float* p = Eh + (u & 15) * S + (u >> 4);
+      const float x = *p - mx;
+      *p = u < n16 ? exp16(x) : (float)exp((double)x);
+    }
+  }
+  __syncthreads();
+  // the reference's sum: lanes 0..15 of the head's wave, chunk order, then
+  // GCC's reduce tree and the tail in order
+  if (mine && lane < 16) {
+    const int nt = n16 >> 4;
+    const float* c = Eh + lane * S;
+    float acc = 0.0f;
+    float4 P[4], Q[4];
+    auto rd = [&](float4* p, int q0) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) p[q] = *(const float4*)(c + q0 + 4 * q);
+    };
+    auto add = [&](const float4* p) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        acc = acc + p[q].x;
+        acc = acc + p[q].y;
+        acc = acc + p[q].z;
+        acc = acc + p[q].w;
+      }
+    };
+    int t = 0;
+    rd(P, 0);
+    for (; t + 32 <= nt; t += 32) {
+      rd(Q, t + 16);
+      __builtin_amdgcn_sched_barrier(0);
+      add(P);
+      __builtin_amdgcn_sched_barrier(0);
+      rd(P, t + 32);
+      __builtin_amdgcn_sched_barrier(0);
+      add(Q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t + 16 <= nt) {
+      add(P);
+      t += 16;
+    }
+    for (; t < nt; t++) acc = acc + c[t];
+    acc = acc + row_ror<8>(acc);
+    acc = acc + row_ror<4>(acc);
+    acc = acc + row_ror<2>(acc);
+    float sum = acc + row_ror<1>(acc);
+    if (lane == 0) {
+      for (int u = n16; u < n; u++) sum += Eh[(u & 15) * S + (u >> 4)];
+      winv[w] = 1.0f / sum;
+    }
+  }
+  __syncthreads();
+  // weights (e * inv) * vs in place, and their maximum
+  if (mine) {
+    const float inv = winv[w];
+    float wm = 0.0f;
+    for (int u = lane; u < n; u += 64) {
+      const int t = G.st + u;
+      float* p = Eh + (u & 15) * S + (u >> 4);
+      const float wt = (*p * inv) * G.vs[G.ring ? t % G.ring : t];
+      *p = wt;
+      wm = __builtin_fmaxf(wm, wt);
+    }
+    wm = wave_max(wm);
+    if (lane == 0) {
+      wqs[w] = wm > 0.0f ? wm / 65535.0f : 0.0f;
+      winv[w] = wm > 0.0f ? 65535.0f / wm : 0.0f;
+    }
+  }
+  __syncthreads();
+
+  // ---- weight planes by slot, every head, four slots per thread
+  const int dom_hi = G.dom_lo + 64 * G.dom_steps;
+  for (int s4 = G.dom_lo + 4 * tid; s4 < dom_hi; s4 += 4 * FUSED_T) {
+    int tt[4];
+    int mult[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int s = s4 + e;
+      mult[e] = (s >= G.lo0 && s < G.hi0) + (G.nrun == 2 && s >= G.lo1 && s < G.hi1);
+      int t;
+      bool ok;
+      if (!G.ring) {
+        t = s, ok = s >= G.st && s < G.en;
+      } else {
+        const int d = ((G.en - 1 - s) % G.ring + G.ring) % G.ring;
+        t = G.en - 1 - d, ok = s < G.ring && t >= G.st;
+      }
+      tt[e] = (ok && mult[e]) ? t - G.st : -1;
+    }
+    int8_t* pb = PL + (size_t)((s4 - G.dom_lo) >> 4) * (48 * grp) + (s4 & 15);
+    for (int hl = 0; hl < grp; hl++) {
+      const float* Ehl = E + (size_t)hl * 16 * S;
+      const bool pos = live_head(hl) && wqs[hl] > 0.0f;
+      uint32_t pa = 0, pbb = 0, pc = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        int W = 0;
+        if (pos && tt[e] >= 0) {
+          const int u = tt[e];
+          int q = (int)__builtin_fmaf(Ehl[(u & 15) * S + (u >> 4)], winv[hl], 0.5f);
+          q = q > 65535 ? 65535 : (q < 0 ? 0 : q);
+          W = mult[e] * q;
+        }
+        pa |= (uint32_t)(W >> 14) << (8 * e);
+        pbb |= (uint32_t)((W >> 7) & 127) << (8 * e);
+        pc |= (uint32_t)(W & 127) << (8 * e);
+      }
+      *(uint32_t*)(pb + hl * 16) = pa;
+      *(uint32_t*)(pb + 16 * grp + hl * 16) = pbb;
+      *(uint32_t*)(pb + 32 * grp + hl * 16) = pc;
+    }
+  }
+  __syncthreads();
+
+  auto mulv = [&](const int* B, int step) {
+    const int8_t* wp = PL + (size_t)(4 * step + q4) * (48 * grp) + hl * 16;
+    v4i Ap[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) Ap[p] = alive ? *(const v4i*)(wp + p * 16 * grp) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < NTW; i++) {
+      const v4i b = {B[4 * i], B[4 * i + 1], B[4 * i + 2], B[4 * i + 3]};
+#pragma unroll
+      for (int p = 0; p < 3; p++) D[p][i] = mfma16(Ap[p], b, D[p][i]);
+    }
+  };
+  for (int st = 0; st < steps; st += 2) {
+    mulv(V0, st);
+    if (st + 2 < steps) loadv(V0, st + 2);
+    if (st + 1 >= steps) break;
+    mulv(V1, st + 1);
+    if (st + 3 < steps) loadv(V1, st + 3);
+  }
+  // out = (float)(a 2^14 + b 2^7 + c) * wmax / 65535
+#pragma unroll
+  for (int i = 0; i < NTW; i++) {
+    const int nt = w + NW * i;
+    if (nt >= HD / 16) continue;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int hr = 4 * (lane >> 4) + k, h = g * grp + hr;
+      if (!live_head(hr)) continue;
+      const uint32_t tot = ((uint32_t)D[0][i][k] << 14) + ((uint32_t)D[1][i][k] << 7) + (uint32_t)D[2][i][k];
+      a.out[((size_t)r * a.nh + h) * HD + 16 * nt + (lane & 15)] = (float)(int32_t)tot * wqs[hr];
+    }
+  }
+}
+
+template <int KS>
+hipError_t launch_fused(const AttnArgs& a, size_t lds, hipStream_t st) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fused_kernel<KS>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL(attn_fused_kernel<KS>, dim3(a.m * a.kvh), dim3(FUSED_T), lds, st, a);
+  return hipGetLastError();
+}
+
 // ----------------------------------------------------------- cache writes
 // fgm_store_v_t (ops.c:653-657)
 __global__ void store_v_t_kernel(int8_t* vt, const int8_t* src, int n, int slot) {
@@ -546,6 +846,24 @@ size_t fgm_attn_layout(AttnArgs* a, void* base, int m, int nh, int kvh, int hd, 
 hipError_t fgm_launch_attn(const AttnArgs& a, int max_n, hipStream_t st) {
   if (a.m <= 0 || a.h1 <= a.h0) return hipSuccess;
   hipError_t e = hipSuccess;
+  // one launch when every row is short and a kv group fits the workgroup;
+  // FGM_ATTN_FUSED=0 keeps the four-launch path (for comparison and tests)
+  const int grp = a.nh / a.kvh;
+  const char* fz = getenv("FGM_ATTN_FUSED");
+  const size_t flds = fused_lds(a.hd, grp, max_n, a.wpl_blocks);
+  if (max_n <= FUSED_MAX_N && grp <= FUSED_MAX_GRP && !(fz && fz[0] == '0') && flds <= 160 * 1024) {
+    switch (a.hd / 64) {
+      case 1: return launch_fused<1>(a, flds, st);
+      case 2: return launch_fused<2>(a, flds, st);
+      case 3: return launch_fused<3>(a, flds, st);
+      case 4: return launch_fused<4>(a, flds, st);
+      case 5: return launch_fused<5>(a, flds, st);
+      case 6: return launch_fused<6>(a, flds, st);
+      case 7: return launch_fused<7>(a, flds, st);
+      case 8: return launch_fused<8>(a, flds, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (max_n > 0) {
     switch (a.hd / 64) {
       case 1: e = launch_scores<1>(a, st); break;

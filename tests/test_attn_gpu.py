@@ -70,10 +70,21 @@ def oracle_out(path, q, kv, nh, st, en, h0, h1, ring, fill=7.0):
     return o, oracle.tail_noncr()
 
 
+@pytest.fixture(params=["auto", "split"])
+def attn_path(request, monkeypatch):
+    """Rows of at most 1024 positions take the single-launch kernel unless
+    FGM_ATTN_FUSED=0 (read per call): run every case both ways."""
+    if request.param == "split":
+        monkeypatch.setenv("FGM_ATTN_FUSED", "0")
+    else:
+        monkeypatch.delenv("FGM_ATTN_FUSED", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("case", cases.ATTN_CASES, ids=[c[0] for c in cases.ATTN_CASES])
-def test_attention_device_matches_reference(case):
+def test_attention_device_matches_reference(case, attn_path):
     name, nh, kvh, hd, cap, ring, st, en, h0, h1, qmul, path = case
-    print(f"attn case {name}", flush=True)
+    print(f"attn case {name} ({attn_path})", flush=True)
     q, kv = cases.attn_inputs(name, nh, kvh, hd, cap, qmul)
     want, noncr = oracle_out(path, q, kv, nh, st, en, h0, h1, ring)
     got = run_device(path, q, kv, nh, st, en, h0, h1, ring)
@@ -97,7 +108,7 @@ def test_attention_dropins_host_pointers(name):
     assert sha(out) == GOLD["attn"][name]["sha256"]
 
 
-def test_long_context_decode():
+def test_long_context_decode(attn_path):
     """A full-attention decode row at head_dim 512 over 8192 positions, and a
     sliding row at head_dim 256 in a ring that has wrapped many times."""
     for name, nh, hd, cap, ring, st, en in (("long512", 8, 512, 8192, 0, 0, 8192),
@@ -108,7 +119,7 @@ def test_long_context_decode():
         same_or_tail_close(got, want, noncr)
 
 
-def test_job_api_batched_decode_and_prefill():
+def test_job_api_batched_decode_and_prefill(attn_path):
     """fgm_hip_attend_dev: three decode sequences (linear, ring, and a short
     one) plus a 40-row prefill chunk with a sliding window in a ring, one
     launch sequence; every row equals the per-row reference computation."""
