@@ -407,6 +407,57 @@ def extra_elem(gpu):
                         "launches (a launch costs >= 1.8 us on this box)", "per_op": res}
 
 
+def extra_prep_fused(gpu):
+    """The GEMM inputs' producers fused into the prep kernel: rmsnorm + prep
+    (before q/k/v and gate/up, hidden 2048) and gelu_mul + prep (before down,
+    FFN 8192), with and without the rotation, one launch, against the two separate launches,
+    at decode (M=8) and prefill (M=256) row counts.  Bytes of the fused form =
+    f32 input(s) + weight + int8 packed output + row scales."""
+    t = gpu.t
+    L, F = gpu.L, gpu.F
+    res = {}
+    for M in (8, 256):
+        # hsz 128: the converter's rotation for every linear (convert_gemma4.py:37)
+        for kind, k, hsz in (("rmsnorm", 2048, 0), ("rmsnorm", 2048, 128), ("gelu_mul", 8192, 128),
+                             ("gelu_mul", 8192, 512)):
+            x = t.randn(M, k, device=gpu.dev)
+            aux = t.randn(k if kind == "rmsnorm" else M * k, device=gpu.dev)
+            mid = t.empty(M, k, device=gpu.dev)
+            qs = t.empty(M, device=gpu.dev)
+            pa = t.empty((M + 15) // 16 * 16 * k, dtype=t.int8, device=gpu.dev)
+            if kind == "rmsnorm":
+                def sep(i):
+                    F.check(L.fgm_hip_rmsnorm_dev(mid.data_ptr(), x.data_ptr(), aux.data_ptr(), M, k,
+                                                  1e-6, gpu.stream()))
+                    F.check(L.fgm_hip_prep_rows_dev(mid.data_ptr(), k, None, None, qs.data_ptr(),
+                                                    pa.data_ptr(), M, k, hsz, 0, M, gpu.stream()))
+
+                def fused(i):
+                    F.check(L.fgm_hip_prep_rmsnorm_dev(x.data_ptr(), k, aux.data_ptr(), 1e-6, None,
+                                                       None, None, qs.data_ptr(), pa.data_ptr(), M,
+                                                       k, hsz, gpu.stream()))
+                nbytes = 4 * M * k + 4 * k + pa.numel() + 4 * M
+            else:
+                def sep(i):
+                    F.check(L.fgm_hip_gelu_mul_dev(mid.data_ptr(), x.data_ptr(), aux.data_ptr(), M * k,
+                                                   gpu.stream()))
+                    F.check(L.fgm_hip_prep_rows_dev(mid.data_ptr(), k, None, None, qs.data_ptr(),
+                                                    pa.data_ptr(), M, k, hsz, 0, M, gpu.stream()))
+
+                def fused(i):
+                    F.check(L.fgm_hip_prep_gelu_mul_dev(x.data_ptr(), aux.data_ptr(), k, None, None,
+                                                        None, qs.data_ptr(), pa.data_ptr(), M, k, hsz,
+                                                        gpu.stream()))
+                nbytes = 8 * M * k + pa.numel() + 4 * M
+            ts = kernel_avg(gpu, sep, 24, 3)
+            tf = kernel_avg(gpu, fused, 24, 3)
+            res[f"{kind}+prep M={M} k={k} hsz={hsz}"] = {
+                "separate_us": ts * 1e6, "fused_us": tf * 1e6, "speedup": ts / tf,
+                "fused_GB_s": nbytes / tf / 1e9, "bytes": nbytes}
+    return {"workload": "producer + prep_rows: two launches vs the fused launch, graphs of 24",
+            "per_op": res}
+
+
 def extra_attn(gpu):
     """int8-KV attention (the forward pass's other hot loop, ops.c:353-877),
     one fgm_hip_attend_dev call (three launches) per layer: batched decode of
@@ -630,7 +681,8 @@ def main():
     gpu = Gpu()
     gpu.t.manual_seed(1234)
     extras = {"cfg1": extra_cfg1, "int4_stream": extra_int4_stream, "cfg3": extra_cfg3,
-              "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem, "attn": extra_attn,
+              "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem,
+              "prep_fused": extra_prep_fused, "attn": extra_attn,
               "model": extra_model}
     if args.only is not None:
         if args.only not in extras:

@@ -74,6 +74,8 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_fwht_hip.argtypes = [p, i, i]
     L.fgm_hip_gemm_batch_dev.argtypes = [p, i, p]
     L.fgm_hip_prep_batch_dev.argtypes = [p, i, p]
+    L.fgm_hip_prep_rmsnorm_dev.argtypes = [p, i, p, f, p, p, p, p, p, i, i, i, p]
+    L.fgm_hip_prep_gelu_mul_dev.argtypes = [p, p, i, p, p, p, p, p, i, i, i, p]
     L.fgm_rmsnorm_hip.argtypes = [p, p, p, i, f]
     L.fgm_rmsnorm_noscale_hip.argtypes = [p, p, i, f]
     L.fgm_gelu_mul_hip.argtypes = [p, p, p, i]
@@ -138,7 +140,9 @@ def _bind(L: _C.CDLL) -> None:
                  "fgm_hip_pool_prep_dev", "fgm_hip_linear_run_dev"):
         getattr(L, name).restype = i
     for name in ("fgm_hip_attend_dev", "fgm_hip_attend_heads_dev", "fgm_hip_store_v_t_dev",
-                 "fgm_hip_kv_store_dev", "fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev", "fgm_hip_gemm_q8c_dev", "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
+                 "fgm_hip_kv_store_dev", "fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev",
+                 "fgm_hip_prep_rmsnorm_dev", "fgm_hip_prep_gelu_mul_dev", "fgm_hip_gemm_q8c_dev",
+                 "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
                  "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path",
                  "fgm_hip_rmsnorm_dev", "fgm_hip_gelu_mul_dev", "fgm_hip_softcap_dev",

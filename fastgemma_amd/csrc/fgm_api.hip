@@ -404,6 +404,43 @@ int fgm_hip_prep_batch_dev(const fgm_hip_prep_desc* d, int count, void* stream) 
   return FGM_HIP_OK;
 }
 
+// One fused problem (rows [0, m)) through the prep kernel.
+static int run_prep_preop(int preop, const float* src, const float* aux, int lda, float eps, float* pre,
+                   float* rot, int8_t* qa, float* qs, int8_t* pa, int m, int k, int hsz,
+                   hipStream_t st, const char* what) {
+  fgm_hip_prep_desc d{src, lda, rot, qa, qs, pa, m, k, hsz, 0, m};
+  if (m < 0) return fail(FGM_HIP_EINVAL, "%s: m=%d", what, m);
+  int rc = check_prep(d);
+  if (rc || m == 0) return rc;
+  if (preop == PREP_GELU_MUL && !aux) return fail(FGM_HIP_EINVAL, "%s: up is NULL", what);
+  if ((rc = ensure_device())) return rc;
+  PrepBatch b{};
+  PrepProb p{src, rot, qa, qs, pa, lda, m, k, hsz, 0, m, fwht_scale(hsz), 0};
+  p.preop = preop;
+  p.aux = aux;
+  p.pre = pre;
+  p.eps = eps;
+  b.p[0] = p;
+  b.count = 1;
+  hipError_t e = fgm_launch_prep(b, st);
+  if (e != hipSuccess) return hip_fail(e, what);
+  return FGM_HIP_OK;
+}
+
+int fgm_hip_prep_rmsnorm_dev(const float* x, int lda, const float* w, float eps, float* xn,
+                             float* rot, int8_t* qa, float* qs, int8_t* pa, int m, int k, int hsz,
+                             void* stream) {
+  return run_prep_preop(PREP_RMSNORM, x, w, lda, eps, xn, rot, qa, qs, pa, m, k, hsz,
+                        (hipStream_t)stream, "prep_rmsnorm");
+}
+
+int fgm_hip_prep_gelu_mul_dev(const float* gate, const float* up, int lda, float* act, float* rot,
+                              int8_t* qa, float* qs, int8_t* pa, int m, int k, int hsz,
+                              void* stream) {
+  return run_prep_preop(PREP_GELU_MUL, gate, up, lda, 0.0f, act, rot, qa, qs, pa, m, k, hsz,
+                        (hipStream_t)stream, "prep_gelu_mul");
+}
+
 int fgm_hip_gemm_batch_dev(const fgm_hip_gemm_desc* d, int count, void* stream) {
   if (count < 0 || (count > 0 && !d)) return fail(FGM_HIP_EINVAL, "gemm batch: bad descriptor array");
   for (int i = 0; i < count; i++) {
@@ -619,7 +656,7 @@ int fgm_hip_softcap_dev(float* x, int n, float cap, void* stream) {
 }
 
 void fgm_hip_rope_table(float* cs, const float* inv_freq, int head_dim, int pos) {
-  // ops.c:133-134, on the host with the host's libm
+  // ops.c:138-139, on the host with the host's libm
   for (int j = 0; j < head_dim / 2; j++) {
     const float a = (float)pos * inv_freq[j];
     cs[2 * j] = cosf(a);

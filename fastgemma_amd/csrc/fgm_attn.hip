@@ -36,28 +36,6 @@
 
 namespace {
 
-// exp512_ps (ops.c:20-38) on one lane
-FGM_DEV float exp16(float x) {
-  x = __builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f);
-  const float fx = __builtin_rintf(x * 1.44269504088896341f);
-  float z = __builtin_fmaf(-fx, 0.693359375f, x);
-  z = __builtin_fmaf(-fx, -2.12194440e-4f, z);
-  float y = 1.9875691500E-4f;
-  y = __builtin_fmaf(y, z, 1.3981999507E-3f);
-  y = __builtin_fmaf(y, z, 8.3334519073E-3f);
-  y = __builtin_fmaf(y, z, 4.1665795894E-2f);
-  y = __builtin_fmaf(y, z, 1.6666665459E-1f);
-  y = __builtin_fmaf(y, z, 5.0000001201E-1f);
-  y = __builtin_fmaf(y, z * z, z);
-  y = y + 1.0f;
-  return y * __int_as_float(((int)fx + 127) << 23);
-}
-
-template <int R>
-FGM_DEV float row_ror(float v) {  // lane j of a 16-lane row reads lane (j + R) % 16
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xF, 0xF, false));
-}
-
 FGM_DEV float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));

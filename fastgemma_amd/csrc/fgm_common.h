@@ -163,3 +163,96 @@ FGM_DEV void sfor(F&& f) {
     sfor<B + 1, E>(f);
   }
 }
+
+// ------------------------------------------------- forward-pass f32 math
+// Shared by the elementwise kernels and the fused prep pre-ops; each
+// reproduces the reference's IEEE operations in the reference's order.
+
+// exp512_ps (ops.c:21-39) on one lane: Cephes range reduction and polynomial.
+FGM_DEV float exp16(float x) {
+  x = __builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f);
+  const float fx = __builtin_rintf(x * 1.44269504088896341f);
+  float z = __builtin_fmaf(-fx, 0.693359375f, x);
+  z = __builtin_fmaf(-fx, -2.12194440e-4f, z);
+  float y = 1.9875691500E-4f;
+  y = __builtin_fmaf(y, z, 1.3981999507E-3f);
+  y = __builtin_fmaf(y, z, 8.3334519073E-3f);
+  y = __builtin_fmaf(y, z, 4.1665795894E-2f);
+  y = __builtin_fmaf(y, z, 1.6666665459E-1f);
+  y = __builtin_fmaf(y, z, 5.0000001201E-1f);
+  y = __builtin_fmaf(y, z * z, z);
+  y = y + 1.0f;
+  return y * __int_as_float(((int)fx + 127) << 23);
+}
+
+// gelu_tanh_v (ops.c:96-107) on one lane, and the scalar tail's form
+// (ops.c:114, 126; GCC fuses v + 0.044715 v^3 into one fma).  The tail's
+// tanhf is evaluated in double and rounded once.
+FGM_DEV float gelu_vec(float x) {
+  const float x3 = (x * x) * x;
+  const float u = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
+  const float e = exp16(u + u);
+  const float t = 1.0f - 2.0f / (e + 1.0f);
+  return (0.5f * x) * (1.0f + t);
+}
+FGM_DEV float tanh_rn(float a) { return (float)tanh((double)a); }
+FGM_DEV float gelu_tail(float v) {
+  return (0.5f * v) * (1.0f + tanh_rn(0.7978845608028654f * __builtin_fmaf((0.044715f * v) * v, v, v)));
+}
+
+template <int R>
+FGM_DEV float row_ror(float v) {  // lane j of a 16-lane row reads lane (j + R) % 16
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+
+// rmsnorm's sum of squares (ops.c:59-91) over a row staged transposed in LDS:
+// x[16 t + j] at lds[j * S + t].  S = 4 (mod 64) puts the 16 accumulator rows
+// in distinct banks, and S >= n / 16 + 16 lets every read-ahead stay in
+// bounds unconditionally.
+__host__ __device__ inline int fgm_rms_stride(int n) { return ((n + 15) / 16 + 16 + 63) / 64 * 64 + 4; }
+
+// Called by lanes 0..15 of one wave (lane j = accumulator j, c = lds + j * S)
+// with nt = n / 16: the reference's 16 fma chains in ascending t, then
+// _mm512_reduce_add_ps as GCC emits it -- t3[j] = p[j + 8] + p[j];
+// t6[j] = t3[j + 4] + t3[j]; (t6[0] + t6[2]) + (t6[1] + t6[3]) -- on DPP row
+// rotations (a + b == b + a exactly, so the pairing is all that matters).
+// Lane 0 returns the vector part's sum.
+FGM_DEV float rms_sumsq16(const float* c, int nt) {
+  float acc = 0.0f;
+  // ping-pong over two sets of four 128-bit reads
+  float4 A[4], B[4];
+  auto rd = [&](float4* r, int t0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) r[q] = *(const float4*)(c + t0 + 4 * q);
+  };
+  auto chain = [&](const float4* r) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      acc = __builtin_fmaf(r[q].x, r[q].x, acc);
+      acc = __builtin_fmaf(r[q].y, r[q].y, acc);
+      acc = __builtin_fmaf(r[q].z, r[q].z, acc);
+      acc = __builtin_fmaf(r[q].w, r[q].w, acc);
+    }
+  };
+  int t = 0;
+  rd(A, 0);
+  for (; t + 32 <= nt; t += 32) {  // the barriers keep each read group ahead of the other's fmas
+    rd(B, t + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    chain(A);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(A, t + 32);
+    __builtin_amdgcn_sched_barrier(0);
+    chain(B);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (t + 16 <= nt) {
+    chain(A);
+    t += 16;
+  }
+  for (; t < nt; t++) acc = __builtin_fmaf(c[t], c[t], acc);
+  acc = acc + row_ror<8>(acc);
+  acc = acc + row_ror<4>(acc);
+  acc = acc + row_ror<2>(acc);
+  return acc + row_ror<1>(acc);
+}

@@ -1,19 +1,19 @@
 // The forward pass's f32 elementwise primitives on gfx950: rmsnorm (with and
 // without scale), gelu / gelu_mul, rope, add / mul / scale and softcap -- the
-// device side of ops.c:17-142, 316-350, keeping activations on the GPU
+// device side of ops.c:15-147, 316-351, keeping activations on the GPU
 // between GEMMs.
 //
 // Every function reproduces the reference's floating-point operations in the
 // reference's order, element for element:
 //   * the reference processes 16 floats per AVX-512 vector and a scalar tail;
-//     the vector part's exp (exp512_ps, ops.c:20-38) is a Cephes polynomial of
+//     the vector part's exp (exp512_ps, ops.c:21-39) is a Cephes polynomial of
 //     IEEE operations and is restated exactly (exp16 below);
 //   * rmsnorm's sum of squares is 16 lane accumulators (lane j takes
 //     x[16 t + j] by fma in ascending t), reduced by GCC's
 //     _mm512_reduce_add_ps tree, then the tail by fma (GCC fuses it);
 //     division and square root are correctly rounded here as on the CPU;
 //   * rope takes its (cos, sin) pairs from the host, computed with the host's
-//     libm exactly as ops.c:133-134 does (fgm_hip_rope_table);
+//     libm exactly as ops.c:138-139 does (fgm_hip_rope_table);
 //   * the scalar tails of gelu and softcap call libm's tanhf on the CPU (not
 //     correctly rounded in glibc 2.35); here tanh is evaluated in double and
 //     rounded once, so the tails agree to libm's own error (a few ulp of
@@ -25,37 +25,6 @@
 #include "fgm_kernels.h"
 
 namespace {
-
-// exp512_ps (ops.c:20-38) on one lane
-FGM_DEV float exp16(float x) {
-  x = __builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f);
-  const float fx = __builtin_rintf(x * 1.44269504088896341f);
-  float z = __builtin_fmaf(-fx, 0.693359375f, x);
-  z = __builtin_fmaf(-fx, -2.12194440e-4f, z);
-  float y = 1.9875691500E-4f;
-  y = __builtin_fmaf(y, z, 1.3981999507E-3f);
-  y = __builtin_fmaf(y, z, 8.3334519073E-3f);
-  y = __builtin_fmaf(y, z, 4.1665795894E-2f);
-  y = __builtin_fmaf(y, z, 1.6666665459E-1f);
-  y = __builtin_fmaf(y, z, 5.0000001201E-1f);
-  y = __builtin_fmaf(y, z * z, z);
-  y = y + 1.0f;
-  return y * __int_as_float(((int)fx + 127) << 23);
-}
-
-// gelu_tanh_v (ops.c:93-104) on one lane, and the scalar tail's form
-// (ops.c:110, 120; GCC fuses v + 0.044715 v^3 into one fma)
-FGM_DEV float gelu_vec(float x) {
-  const float x3 = (x * x) * x;
-  const float u = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
-  const float e = exp16(u + u);
-  const float t = 1.0f - 2.0f / (e + 1.0f);
-  return (0.5f * x) * (1.0f + t);
-}
-FGM_DEV float tanh_rn(float a) { return (float)tanh((double)a); }
-FGM_DEV float gelu_tail(float v) {
-  return (0.5f * v) * (1.0f + tanh_rn(0.7978845608028654f * __builtin_fmaf((0.044715f * v) * v, v, v)));
-}
 
 // --------------------------------------------------------------- rmsnorm
 // One workgroup per row; the row's latency is the whole cost at the forward
@@ -73,11 +42,6 @@ FGM_DEV float gelu_tail(float v) {
 // The variant for n % 4 != 0 or unaligned rows keeps nothing in registers:
 // x goes straight to LDS and w is read at the end.
 constexpr int RMS_MAXV = 8;  // float4 slots per thread (n <= 32 T)
-
-template <int R>
-FGM_DEV float row_ror(float v) {  // lane j of a 16-lane row reads lane (j + R) % 16
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xF, 0xF, false));
-}
 
 template <bool VEC>
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* out, const float* x, const float* w, int n, int S,
@@ -118,48 +82,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(float* out, const float* 
   }
   __syncthreads();
   if (tid < 16) {
-    const int nt = n >> 4;
-    const float* c = lds + tid * S;
-    float acc = 0.0f;
-    // ping-pong over two sets of four 128-bit reads; the rows are padded
-    // (S >= nt + 16) so every prefetch is unconditional and in bounds.
-    float4 A[4], B[4];
-    auto rd = [&](float4* r, int t0) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) r[q] = *(const float4*)(c + t0 + 4 * q);
-    };
-    auto chain = [&](const float4* r) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        acc = __builtin_fmaf(r[q].x, r[q].x, acc);
-        acc = __builtin_fmaf(r[q].y, r[q].y, acc);
-        acc = __builtin_fmaf(r[q].z, r[q].z, acc);
-        acc = __builtin_fmaf(r[q].w, r[q].w, acc);
-      }
-    };
-    int t = 0;
-    rd(A, 0);
-    for (; t + 32 <= nt; t += 32) {  // the barriers keep each read group ahead of the other's fmas
-      rd(B, t + 16);
-      __builtin_amdgcn_sched_barrier(0);
-      chain(A);
-      __builtin_amdgcn_sched_barrier(0);
-      rd(A, t + 32);
-      __builtin_amdgcn_sched_barrier(0);
-      chain(B);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (t + 16 <= nt) {
-      chain(A);
-      t += 16;
-    }
-    for (; t < nt; t++) acc = __builtin_fmaf(c[t], c[t], acc);
-    // _mm512_reduce_add_ps: t3[j] = p[j + 8] + p[j]; t6[j] = t3[j + 4] + t3[j];
-    // (t6[0] + t6[2]) + (t6[1] + t6[3])
-    acc = acc + row_ror<8>(acc);
-    acc = acc + row_ror<4>(acc);
-    acc = acc + row_ror<2>(acc);
-    float ss = acc + row_ror<1>(acc);
+    float ss = rms_sumsq16(lds + tid * S, n >> 4);
     if (tid == 0) {
       for (int i = n & ~15; i < n; i++) {
         const float v = lds[(i & 15) * S + (i >> 4)];
@@ -260,7 +183,7 @@ hipError_t fgm_launch_rmsnorm(float* out, const float* x, const float* w, int ro
   // about two float4 slots per thread; at most RMS_MAXV (n <= 32 T, T <= 1024)
   const int T = std::min(1024, std::max(64, ((n + 7) / 8 + 63) / 64 * 64));
   if (n > 32 * T) return hipErrorInvalidValue;
-  const int S = ((n + 15) / 16 + 16 + 63) / 64 * 64 + 4;  // S = 4 (mod 64), >= n / 16 + 16
+  const int S = fgm_rms_stride(n);
   const size_t lds = ((size_t)16 * S + 4) * 4;
   const bool vec = n % 4 == 0 && (((uintptr_t)out | (uintptr_t)x | (uintptr_t)w) & 15) == 0;
   if (vec)

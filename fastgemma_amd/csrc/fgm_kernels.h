@@ -37,13 +37,24 @@ struct PrepProb {
   int lda, m, k, hsz, r0, r1;
   float fwht_scale;
   int wg0;         // first workgroup (set by the launcher)
+  // fused producer applied to each row before the rotation (one kind per
+  // batch): PREP_RMSNORM normalises src by aux (NULL: no scale) with eps;
+  // PREP_GELU_MUL takes gelu(src) * aux, aux rows lda apart.  pre, when set,
+  // receives that result as [m][k] (the reference's xn / act buffer).
+  int preop;
+  const float* aux;
+  float* pre;
+  float eps;
 };
+enum { PREP_COPY = 0, PREP_RMSNORM = 1, PREP_GELU_MUL = 2 };
 
 struct PrepBatch {
   PrepProb p[FGM_MAX_BATCH];
   int count;
 };
 
+// Every problem of a batch has the same preop; a preop needs k % 64 == 0 (no
+// scalar tails).
 hipError_t fgm_launch_prep(const PrepBatch& b, hipStream_t st);
 hipError_t fgm_launch_pack_a(int M, int K, const int8_t* A, int8_t* Ap, hipStream_t st);
 hipError_t fgm_launch_fwht(float* x, int n, int hsz, float scale, hipStream_t st);

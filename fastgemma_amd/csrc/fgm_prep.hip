@@ -1,6 +1,11 @@
 // GEMM activation preamble on gfx950: copy, optional FWHT, per-row int8
 // quantisation and A tile-packing -- the device side of fgm_prep_rows,
 // fgm_quant_act, fgm_fwht and fgm_pack_a (ops.c:153-204, 279-314).
+// Optionally the row's producer runs first in the same workgroup: rmsnorm
+// (ops.c:59-91, before the q/k/v and gate/up GEMMs, forward.rs:477-481,
+// 614-618) or gelu_mul (ops.c:119-128, before down, forward.rs:621-622),
+// with the reference's operations in its order, so the bytes equal the two
+// separate calls'.
 //
 // One workgroup owns one activation row; each thread holds up to VMAX
 // consecutive float4s of it (vector i = thread + v * blockDim covers columns
@@ -10,6 +15,8 @@
 // maximum is a wave reduction plus one LDS exchange (order-free for non-NaN
 // rows); then each float4 becomes one dword of the row-major int8 copy and
 // one dword of its packed tile.
+#include <algorithm>
+
 #include "fgm_common.h"
 #include "fgm_kernels.h"
 
@@ -18,12 +25,11 @@ namespace {
 constexpr int PREP_MAX_THREADS = 1024;
 constexpr int VMAX = 8;  // float4s per thread: rows up to 8 * 4 * 1024 = 32768 floats
 
-// In-place normalised FWHT of the `k` floats in LDS, blocks of `hsz` (a power
-// of two; ops.c:153-175).  `scale` = 1/sqrtf(hsz) computed on the host; it is
-// only applied for hsz >= 16, matching the reference's 16-wide scale loop.
-__device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
+// The butterfly stages of distance 2^lg0 .. hsz / 2 of the FWHT of the `k`
+// floats in LDS, blocks of `hsz` (a power of two; ops.c:153-175).
+__device__ void fwht_lds_stages(float* buf, int k, int hsz, int lg0) {
   const int half = k >> 1;
-  for (int lg = 0; (1 << lg) < hsz; lg++) {
+  for (int lg = lg0; (1 << lg) < hsz; lg++) {
     const int len = 1 << lg;
     for (int p = threadIdx.x; p < half; p += blockDim.x) {
       const int i = ((p >> lg) << (lg + 1)) | (p & (len - 1));  // pairs never straddle a block
@@ -33,10 +39,30 @@ __device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
     }
     __syncthreads();
   }
+}
+
+// In-place normalised FWHT in LDS.  `scale` = 1/sqrtf(hsz) computed on the
+// host; it is only applied for hsz >= 16, matching the reference's 16-wide
+// scale loop.
+__device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
+  fwht_lds_stages(buf, k, hsz, 0);
   if (hsz >= 16) {
     for (int i = threadIdx.x; i < k; i += blockDim.x) buf[i] = buf[i] * scale;
     __syncthreads();
   }
+}
+
+// The value lane ^ L of the wave holds (L < 64): DPP quad permutes for 1 and
+// 2, a row rotation for 8, ds_swizzle's xor mode (within 32 lanes) for 4 and
+// 16, ds_bpermute for 32.
+template <int L>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int b = __float_as_int(v);
+  if constexpr (L == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+  else if constexpr (L == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+  else if constexpr (L == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
+  else if constexpr (L < 32) return __int_as_float(__builtin_amdgcn_ds_swizzle(b, (L << 10) | 0x1F));
+  else return __shfl_xor(v, L, 64);
 }
 
 // Maximum over the 64 lanes of a wave: DPP within each 16-lane row, then the
@@ -73,6 +99,7 @@ __device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
   return p;
 }
 
+template <int PRE>
 __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
   __shared__ float red[PREP_MAX_THREADS / 64];
@@ -101,10 +128,13 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   const float* src = a.src + (size_t)row * a.lda;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)k * 4);
   const bool vec = ((((uintptr_t)a.src) & 15) == 0) && (a.lda & 3) == 0 && (k & 3) == 0;
+  // float4s per thread that reach into the row (uniform)
+  const int nv = ((k + 3) / 4 + T - 1) / T;
   float x[VMAX][4];
   if (vec) {
 #pragma unroll
     for (int v = 0; v < VMAX; v++) {
+      if (v >= nv) break;
       const int c = 4 * (tid + v * T);
       const v4i q = buf_load_b128(rs, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
 #pragma unroll
@@ -113,6 +143,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   } else {
 #pragma unroll
     for (int v = 0; v < VMAX; v++) {
+      if (v >= nv) break;
       const int c = 4 * (tid + v * T);
 #pragma unroll
       for (int e = 0; e < 4; e++)
@@ -120,31 +151,184 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     }
   }
 
-  // 2. optional rotation, through LDS
-  if (a.hsz > 0) {
+  // 1b. the fused producer (k % 64 == 0 here: the reference's vector forms
+  //     cover the whole row, no scalar tails)
+  if constexpr (PRE == PREP_RMSNORM) {
+    // w is loaded before the reduction so its latency hides behind it
+    float w[VMAX][4];
+    if (a.aux) {
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.aux, (uint32_t)k * 4);
+      const bool wvec = (((uintptr_t)a.aux) & 15) == 0;
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const int c = 4 * (tid + v * T);
+        if (wvec) {
+          const v4i q = buf_load_b128(rw, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
+#pragma unroll
+          for (int e = 0; e < 4; e++) w[v][e] = __int_as_float(q[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            w[v][e] = __int_as_float(buf_load_b32(rw, c + e < k ? (uint32_t)(c + e) * 4 : FGM_OOB, 0));
+        }
+      }
+    }
+    // the row transposed, x[16 t + j] at buf[j * S + t], for the 16 chains:
+    // float4 i4 (columns 4 i4 .. 4 i4 + 3) goes to rows 4 (i4 % 4) + e,
+    // column i4 / 4 (k % 4 == 0, so a float4 is wholly in or out of the row)
+    const int S = fgm_rms_stride(k);
+    auto tpos = [&](int i4) { return buf + 4 * (i4 & 3) * S + (i4 >> 2); };
 #pragma unroll
     for (int v = 0; v < VMAX; v++) {
-      const int c = 4 * (tid + v * T);
+      if (v >= nv) break;
+      const int i4 = tid + v * T;
+      if (4 * i4 < k) {
+        float* p = tpos(i4);
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (c + e < k) buf[c + e] = x[v][e];
+        for (int e = 0; e < 4; e++) p[e * S] = x[v][e];
+      }
     }
     __syncthreads();
-    fwht_lds(buf, k, a.hsz, a.fwht_scale);
+    if (tid < 16) {
+      const float ss = rms_sumsq16(buf + tid * S, k >> 4);
+      if (tid == 0) buf[16 * S] = 1.0f / __builtin_sqrtf(ss / (float)k + a.eps);
+    }
+    __syncthreads();
+    // buf[16 * S] lies beyond the k floats a rotation stages below.  x is
+    // read back from LDS so that it is not live in registers across the
+    // reduction (w and the chains' read-ahead already need them).
+    const float rinv = buf[16 * S];
 #pragma unroll
     for (int v = 0; v < VMAX; v++) {
-      const int c = 4 * (tid + v * T);
+      if (v >= nv) break;
+      const int i4 = tid + v * T;
+      const float* p = tpos(i4);
 #pragma unroll
-      for (int e = 0; e < 4; e++) x[v][e] = (c + e < k) ? buf[c + e] : 0.0f;
+      for (int e = 0; e < 4; e++) {
+        const float xi = 4 * i4 < k ? p[e * S] : 0.0f;
+        x[v][e] = a.aux ? (xi * rinv) * w[v][e] : xi * rinv;
+      }
+    }
+  }
+  if constexpr (PRE == PREP_GELU_MUL) {
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.aux + (size_t)row * a.lda, (uint32_t)k * 4);
+    const bool uvec = ((((uintptr_t)a.aux) & 15) == 0) && (a.lda & 3) == 0;
+#pragma unroll
+    for (int v = 0; v < VMAX; v++) {
+      if (v >= nv) break;
+      const int c = 4 * (tid + v * T);
+      float u[4];
+      if (uvec) {
+        const v4i q = buf_load_b128(ru, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
+#pragma unroll
+        for (int e = 0; e < 4; e++) u[e] = __int_as_float(q[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          u[e] = __int_as_float(buf_load_b32(ru, c + e < k ? (uint32_t)(c + e) * 4 : FGM_OOB, 0));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) x[v][e] = gelu_vec(x[v][e]) * u[e];  // 0 past k
+    }
+  }
+  if constexpr (PRE != PREP_COPY) {
+    if (a.pre) {
+      float* o = a.pre + (size_t)row * k;
+      const bool ovec = (((uintptr_t)a.pre) & 15) == 0;
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const int c = 4 * (tid + v * T);
+        if (c >= k) break;
+        if (ovec) {
+          *(float4*)(o + c) = make_float4(x[v][0], x[v][1], x[v][2], x[v][3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) o[c + e] = x[v][e];
+        }
+      }
+    }
+  }
+
+  // 2. optional rotation.  Element c = 4 i4 + e sits in lane i4 % 64 of its
+  //    wave (T is a multiple of 64, so a wave holds 64 consecutive float4s):
+  //    stages of distance 1 and 2 stay in the thread, 4 .. 128 pair lanes of
+  //    one wave, 256 and up go through LDS.  Each stage is one add (lower
+  //    element) or one subtract (upper element) of the same two values in
+  //    every schedule, so the bytes are the reference's.
+  if (a.hsz > 0) {
+    const int hsz = a.hsz;
+    const int lane = tid & 63;
+    if (hsz > 1) {
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const float u0 = x[v][0], u1 = x[v][1], u2 = x[v][2], u3 = x[v][3];
+        x[v][0] = u0 + u1, x[v][1] = u0 - u1, x[v][2] = u2 + u3, x[v][3] = u2 - u3;
+      }
+    }
+    if (hsz > 2) {
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const float u0 = x[v][0], u1 = x[v][1], u2 = x[v][2], u3 = x[v][3];
+        x[v][0] = u0 + u2, x[v][1] = u1 + u3, x[v][2] = u0 - u2, x[v][3] = u1 - u3;
+      }
+    }
+    sfor<0, 6>([&](auto J) {
+      constexpr int L = 1 << J;  // partner lane distance; element distance 4 L
+      if (hsz > 4 * L) {
+        const bool upper = lane & L;
+#pragma unroll
+        for (int v = 0; v < VMAX; v++) {
+          if (v >= nv) break;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float y = lane_xor<L>(x[v][e]);
+            x[v][e] = upper ? y - x[v][e] : x[v][e] + y;
+          }
+        }
+      }
+    });
+    if (hsz > 256) {
+      if constexpr (PRE == PREP_RMSNORM) __syncthreads();  // x was re-read from buf
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const int c = 4 * (tid + v * T);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (c + e < k) buf[c + e] = x[v][e];
+      }
+      __syncthreads();
+      fwht_lds_stages(buf, k, hsz, 8);
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+        const int c = 4 * (tid + v * T);
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[v][e] = (c + e < k) ? buf[c + e] : 0.0f;
+      }
+    }
+    if (hsz >= 16) {
+#pragma unroll
+      for (int v = 0; v < VMAX; v++) {
+        if (v >= nv) break;
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[v][e] = x[v][e] * a.fwht_scale;
+      }
     }
   }
 
   // 3. absolute maximum of the row
   float mx = 0.0f;
 #pragma unroll
-  for (int v = 0; v < VMAX; v++)
+  for (int v = 0; v < VMAX; v++) {
+    if (v >= nv) break;
 #pragma unroll
     for (int e = 0; e < 4; e++) mx = fmaxf(mx, __builtin_fabsf(x[v][e]));
+  }
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
@@ -162,6 +346,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   const bool dw = (k & 3) == 0;  // rows of qa / rot start 4-byte aligned
 #pragma unroll
   for (int v = 0; v < VMAX; v++) {
+    if (v >= nv) break;
     const int c = 4 * (tid + v * T);
     if (c >= k) break;
     uint32_t packed;
@@ -241,28 +426,45 @@ static hipError_t allow_big_lds(K kernel) {
 }
 
 hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
-  static hipError_t attr = allow_big_lds(prep_rows_kernel);
-  if (attr != hipSuccess) return attr;
+  static hipError_t attr[3] = {allow_big_lds(prep_rows_kernel<PREP_COPY>),
+                               allow_big_lds(prep_rows_kernel<PREP_RMSNORM>),
+                               allow_big_lds(prep_rows_kernel<PREP_GELU_MUL>)};
   PrepBatch b = in;
-  int nwg = 0, kmax = 0, kfwht = 0;
+  const int pre = b.count ? b.p[0].preop : PREP_COPY;
+  if (pre < PREP_COPY || pre > PREP_GELU_MUL) return hipErrorInvalidValue;
+  if (attr[pre] != hipSuccess) return attr[pre];
+  int nwg = 0, kmax = 0, lds_floats = 0;
   for (int i = 0; i < b.count; i++) {
     PrepProb& p = b.p[i];
+    if (p.preop != pre || (pre != PREP_COPY && p.k % 64)) return hipErrorInvalidValue;
     p.wg0 = nwg;
     if (p.r0 < p.r1) {
       // rows [r0, r1) compute; rows [r1, end of r1's tile block) only pack
       const int end = p.pa ? ((p.r1 + 15) / 16) * 16 : p.r1;
       nwg += end - p.r0;
       if (p.k > kmax) kmax = p.k;
-      if (p.hsz > 0 && p.k > kfwht) kfwht = p.k;
+      if (p.hsz > 0 && p.k > lds_floats) lds_floats = p.k;
+      // the transposed row plus 1/rms (16 S + 1 > k floats)
+      if (pre == PREP_RMSNORM) lds_floats = std::max(lds_floats, 16 * fgm_rms_stride(p.k) + 4);
     }
   }
   if (nwg == 0) return hipSuccess;
-  // up to VMAX float4s per thread (fewer waves: a cheaper row reduction),
-  // whole waves, at most 1024 threads
-  int threads = ((kmax + 4 * VMAX - 1) / (4 * VMAX) + 63) / 64 * 64;
-  if (threads < 64) threads = 64;
-  if (threads > PREP_MAX_THREADS) threads = PREP_MAX_THREADS;
-  hipLaunchKernelGGL(prep_rows_kernel, dim3(nwg), dim3(threads), (size_t)kfwht * sizeof(float), st, b);
+  // One float4 per thread up to 512 threads (gelu_mul, heavier per element:
+  // 1024), more float4s per thread beyond, at most VMAX: a row's work is
+  // latency-bound at the decode sizes, so more waves per row pay until the
+  // cross-wave reduction costs more than they save (measured: 512 threads
+  // for k = 2048 .. 8192).  Whole waves.
+  const int cap = pre == PREP_GELU_MUL ? PREP_MAX_THREADS : 512;
+  int threads = std::min(cap, ((kmax + 3) / 4 + 63) / 64 * 64);
+  threads = std::max(threads, ((kmax + 4 * VMAX - 1) / (4 * VMAX) + 63) / 64 * 64);
+  threads = std::max(64, std::min(threads, PREP_MAX_THREADS));
+  const size_t lds = (size_t)lds_floats * sizeof(float);
+  if (pre == PREP_RMSNORM)
+    hipLaunchKernelGGL(prep_rows_kernel<PREP_RMSNORM>, dim3(nwg), dim3(threads), lds, st, b);
+  else if (pre == PREP_GELU_MUL)
+    hipLaunchKernelGGL(prep_rows_kernel<PREP_GELU_MUL>, dim3(nwg), dim3(threads), lds, st, b);
+  else
+    hipLaunchKernelGGL(prep_rows_kernel<PREP_COPY>, dim3(nwg), dim3(threads), lds, st, b);
   return hipGetLastError();
 }
 

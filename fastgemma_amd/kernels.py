@@ -165,6 +165,32 @@ def prep_rows(src, lda, rot, qa, qs, pa, m, k, hsz, r0, r1) -> None:
                                           m, k, hsz, r0, r1, _stream()))
 
 
+def _opt(t):
+    return _dp(t) if t is not None else None
+
+
+def prep_rmsnorm(x, lda: int, w, eps: float, qs, pa, m: int, k: int, hsz: int, xn=None, rot=None,
+                 qa=None, stream=None) -> None:
+    """rmsnorm (w None: rmsnorm_noscale) fused with prep_rows over rows
+    [0, m) of x: the bytes of rmsnorm (lib.rs:220-228) per row into xn
+    followed by prep_rows(xn, k, ...) (lib.rs:517-529), in one launch
+    (device tensors; xn, rot and qa are optional outputs)."""
+    backend()
+    check(lib().fgm_hip_prep_rmsnorm_dev(_dp(x), lda, _opt(w), eps, _opt(xn), _opt(rot), _opt(qa),
+                                         _dp(qs), _dp(pa), m, k, hsz,
+                                         _stream() if stream is None else stream))
+
+
+def prep_gelu_mul(gate, up, lda: int, qs, pa, m: int, k: int, hsz: int, act=None, rot=None,
+                  qa=None, stream=None) -> None:
+    """gelu_mul (lib.rs:231-233) fused with prep_rows over rows [0, m)
+    (device tensors; act, rot and qa are optional outputs)."""
+    backend()
+    check(lib().fgm_hip_prep_gelu_mul_dev(_dp(gate), _dp(up), lda, _opt(act), _opt(rot), _opt(qa),
+                                          _dp(qs), _dp(pa), m, k, hsz,
+                                          _stream() if stream is None else stream))
+
+
 # ------------------------------------------------- device-only extensions
 def acc_q8c(m, n, k, a, b, acc, ldacc, n0, n1) -> None:
     """Raw int32 accumulators of the q8c GEMM (device tensors)."""
@@ -273,7 +299,7 @@ def gelu(x) -> None:
 
 def rope_table(inv_freq: np.ndarray, head_dim: int, pos: int) -> np.ndarray:
     """(cos, sin) pairs for one position, computed on the host with the
-    host's libm exactly as ops.c:133-134 does: float32 [head_dim // 2, 2]."""
+    host's libm exactly as ops.c:138-139 does: float32 [head_dim // 2, 2]."""
     inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
     cs = np.empty((head_dim // 2, 2), np.float32)
     lib().fgm_hip_rope_table(cs.ctypes.data, inv.ctypes.data, head_dim, pos)

@@ -134,21 +134,21 @@ int fgm_hip_fwht_dev(float *x, int n, int hsz, void *stream);
  * within a few ulp; no model dimension has such a tail). */
 
 /* drop-ins, host pointers, same parameters as the reference's symbols */
-void fgm_rmsnorm_hip(float *out, const float *x, const float *w, int n, float eps); /* lib.rs:47, ops.c:55-71 */
-void fgm_rmsnorm_noscale_hip(float *out, const float *x, int n, float eps);        /* lib.rs:48, ops.c:74-88 */
-void fgm_gelu_mul_hip(float *out, const float *gate, const float *up, int n);       /* lib.rs:49, ops.c:115-124 */
-void fgm_gelu_hip(float *x, int n);                                                 /* lib.rs:50, ops.c:106-112 */
-void fgm_rope_hip(float *x, int n_heads, int head_dim, const float *inv_freq, int pos); /* lib.rs:51, ops.c:130-142 */
-void fgm_add_hip(float *a, const float *b, int n);                                  /* lib.rs:56, ops.c:316-321 */
-void fgm_mul_hip(float *a, const float *b, int n);                                  /* lib.rs:57, ops.c:323-328 */
-void fgm_scale_hip(float *a, float s, int n);                                       /* lib.rs:58, ops.c:330-336 */
-void fgm_softcap_hip(float *x, int n, float cap);                                   /* lib.rs:59, ops.c:338-350 */
+void fgm_rmsnorm_hip(float *out, const float *x, const float *w, int n, float eps); /* lib.rs:47, ops.c:59-74 */
+void fgm_rmsnorm_noscale_hip(float *out, const float *x, int n, float eps);        /* lib.rs:48, ops.c:77-91 */
+void fgm_gelu_mul_hip(float *out, const float *gate, const float *up, int n);       /* lib.rs:49, ops.c:119-128 */
+void fgm_gelu_hip(float *x, int n);                                                 /* lib.rs:50, ops.c:109-116 */
+void fgm_rope_hip(float *x, int n_heads, int head_dim, const float *inv_freq, int pos); /* lib.rs:51, ops.c:135-147 */
+void fgm_add_hip(float *a, const float *b, int n);                                  /* lib.rs:56, ops.c:317-322 */
+void fgm_mul_hip(float *a, const float *b, int n);                                  /* lib.rs:57, ops.c:324-329 */
+void fgm_scale_hip(float *a, float s, int n);                                       /* lib.rs:58, ops.c:331-337 */
+void fgm_softcap_hip(float *x, int n, float cap);                                   /* lib.rs:59, ops.c:340-351 */
 
 /* device API: rmsnorm of `rows` contiguous rows of n floats each (w NULL:
  * no scale, fgm_rmsnorm_noscale); gelu_mul with up NULL is gelu (out may be
  * gate); rope on x [rows][n_heads][head_dim] with cs [rows][head_dim/2][2] =
  * (cos, sin) pairs from fgm_hip_rope_table (host, the host's libm, as
- * ops.c:133-134); add / mul / scale in place on a. */
+ * ops.c:138-139); add / mul / scale in place on a. */
 int fgm_hip_rmsnorm_dev(float *out, const float *x, const float *w, int rows, int n, float eps,
                         void *stream);
 int fgm_hip_gelu_mul_dev(float *out, const float *gate, const float *up, int n, void *stream);
@@ -358,6 +358,23 @@ typedef struct fgm_hip_prep_desc {
 } fgm_hip_prep_desc;
 
 int fgm_hip_prep_batch_dev(const fgm_hip_prep_desc *descs, int count, void *stream);
+
+/* A GEMM input's producer fused into fgm_prep_rows over rows [0, m): the
+ * result is byte-identical to the producer followed by
+ * fgm_hip_prep_rows_dev(xn_or_act, k, rot, qa, qs, pa, m, k, hsz, 0, m).
+ * Same constraints as prep_rows (k % 64 == 0, k <= 32768); xn / act, rot and
+ * qa may be NULL; rows of the last tile block past m are zero in pa.
+ *   rmsnorm:  fgm_rmsnorm / fgm_rmsnorm_noscale (w NULL) of each row of x
+ *             (row stride lda), as the forward pass does before the q/k/v
+ *             and gate/up GEMMs (forward.rs:477-481, 614-618; ops.c:59-91);
+ *   gelu_mul: gelu(gate) * up (both row stride lda), before the down GEMM
+ *             (forward.rs:621-622; ops.c:119-128). */
+int fgm_hip_prep_rmsnorm_dev(const float *x, int lda, const float *w, float eps, float *xn,
+                             float *rot, int8_t *qa, float *qs, int8_t *pa, int m, int k,
+                             int hsz, void *stream);
+int fgm_hip_prep_gelu_mul_dev(const float *gate, const float *up, int lda, float *act,
+                              float *rot, int8_t *qa, float *qs, int8_t *pa, int m, int k,
+                              int hsz, void *stream);
 
 #ifdef __cplusplus
 }

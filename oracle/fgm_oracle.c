@@ -432,7 +432,7 @@ void orc_gen_student_t(uint64_t seed, size_t n, int nu, float *out) {
 }
 
 /* ======================================================= elementwise ops
- * The forward pass's f32 elementwise primitives, ops.c:17-38 (exp512_ps),
+ * The forward pass's f32 elementwise primitives, ops.c:15-39 (exp512_ps),
  * :55-88 (rmsnorm), :90-124 (gelu), :126-142 (rope), :316-350 (add, mul,
  * scale, softcap).  The reference processes 16 floats per AVX-512 vector and
  * finishes with a scalar tail; both parts are restated element by element in
@@ -441,7 +441,7 @@ void orc_gen_student_t(uint64_t seed, size_t n, int nu, float *out) {
  * expressions into one fma.  Where it does (determined against the compiled
  * reference, tests/test_elem.py), this restatement writes fmaf explicitly. */
 
-/* exp512_ps (ops.c:20-38) on one lane: Cephes range reduction. */
+/* exp512_ps (ops.c:21-39) on one lane: Cephes range reduction. */
 float orc_exp16(float x) {
   x = fminf(fmaxf(x, -88.0f), 88.0f);
   const float fx = rintf(x * 1.44269504088896341f); /* _mm512_roundscale_ps, RNE */
@@ -472,7 +472,7 @@ static float gcc_reduce_add16(const float *a) {
   return (t6[0] + t6[2]) + (t6[1] + t6[3]);
 }
 
-/* sum of squares and 1/rms of one row (ops.c:58-66, 75-83): 16 lane
+/* sum of squares and 1/rms of one row (ops.c:60-67, 78-85): 16 lane
  * accumulators, lane j takes x[16t + j] in ascending t by fma; GCC's tree;
  * the tail fused as fmaf(x, x, ss); then 1 / sqrtf(ss / n + eps). */
 static float rms_inv(const float *x, int n, float eps) {
@@ -485,19 +485,19 @@ static float rms_inv(const float *x, int n, float eps) {
   return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-/* fgm_rmsnorm (ops.c:55-71): out = (x * inv) * w */
+/* fgm_rmsnorm (ops.c:59-74): out = (x * inv) * w */
 void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
   const float inv = rms_inv(x, n, eps);
   for (int i = 0; i < n; i++) out[i] = (x[i] * inv) * w[i];
 }
 
-/* fgm_rmsnorm_noscale (ops.c:74-88): out = x * inv */
+/* fgm_rmsnorm_noscale (ops.c:77-91): out = x * inv */
 void orc_rmsnorm_noscale(float *out, const float *x, int n, float eps) {
   const float inv = rms_inv(x, n, eps);
   for (int i = 0; i < n; i++) out[i] = x[i] * inv;
 }
 
-/* gelu_tanh_v (ops.c:93-104) on one lane */
+/* gelu_tanh_v (ops.c:96-107) on one lane */
 static float gelu_vec(float x) {
   const float x3 = (x * x) * x;
   const float u = 0.7978845608028654f * fmaf(0.044715f, x3, x);
@@ -506,25 +506,25 @@ static float gelu_vec(float x) {
   return (0.5f * x) * (1.0f + t);
 }
 
-/* the scalar tail's gelu (ops.c:110, 120): libm tanhf; GCC fuses
+/* the scalar tail's gelu (ops.c:114, 126): libm tanhf; GCC fuses
  * v + 0.044715f * v * v * v into fmaf((0.044715f * v) * v, v, v) */
 static float gelu_tail(float v) {
   return (0.5f * v) * (1.0f + tanhf(0.7978845608028654f * fmaf((0.044715f * v) * v, v, v)));
 }
 
-/* fgm_gelu_mul (ops.c:115-124): out = gelu(gate) * up */
+/* fgm_gelu_mul (ops.c:119-128): out = gelu(gate) * up */
 void orc_gelu_mul(float *out, const float *gate, const float *up, int n) {
   const int nv = n & ~15;
   for (int i = 0; i < n; i++) out[i] = (i < nv ? gelu_vec(gate[i]) : gelu_tail(gate[i])) * up[i];
 }
 
-/* fgm_gelu (ops.c:106-112), in place */
+/* fgm_gelu (ops.c:109-116), in place */
 void orc_gelu(float *x, int n) {
   const int nv = n & ~15;
   for (int i = 0; i < n; i++) x[i] = i < nv ? gelu_vec(x[i]) : gelu_tail(x[i]);
 }
 
-/* fgm_rope (ops.c:130-142): a = pos * inv_freq[j], c = cosf(a), s = sinf(a)
+/* fgm_rope (ops.c:135-147): a = pos * inv_freq[j], c = cosf(a), s = sinf(a)
  * (libm); GCC fuses the rotation into fmaf(lo, c, -(hi * s)) and
  * fmaf(hi, c, lo * s). */
 void orc_rope(float *x, int n_heads, int head_dim, const float *inv_freq, int pos) {
@@ -541,12 +541,12 @@ void orc_rope(float *x, int n_heads, int head_dim, const float *inv_freq, int po
   }
 }
 
-/* fgm_add / fgm_mul / fgm_scale (ops.c:316-336) */
+/* fgm_add / fgm_mul / fgm_scale (ops.c:317-337) */
 void orc_add(float *a, const float *b, int n) { for (int i = 0; i < n; i++) a[i] += b[i]; }
 void orc_mul(float *a, const float *b, int n) { for (int i = 0; i < n; i++) a[i] *= b[i]; }
 void orc_scale(float *a, float s, int n) { for (int i = 0; i < n; i++) a[i] *= s; }
 
-/* fgm_softcap (ops.c:338-350): vector part cap * (1 - 2 / (exp(2u) + 1)) with
+/* fgm_softcap (ops.c:340-351): vector part cap * (1 - 2 / (exp(2u) + 1)) with
  * u = x * (1 / cap); tail cap * tanhf(x / cap) */
 void orc_softcap(float *x, int n, float cap) {
   const float ci = 1.0f / cap;

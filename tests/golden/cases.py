@@ -178,7 +178,7 @@ def elem_inputs(n: int):
 
 
 # RoPE: a Gemma-style proportional table (theta 1e6, the last quarter of the
-# half-dimension zero: "nope" dims pass through, ops.c:127-129), 8 heads.
+# half-dimension zero: "nope" dims pass through, ops.c:133-134), 8 heads.
 ROPE_CASES = [(8, 256, 0), (8, 256, 1), (8, 256, 997), (4, 512, 32767), (2, 64, 5)]
 
 

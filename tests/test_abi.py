@@ -76,6 +76,15 @@ def test_other_preconditions():
     assert L.fgm_hip_fwht_dev(None, 96, 12, None) == 1
     assert L.fgm_hip_fwht_dev(None, 96, 64, None) == 1
     assert L.fgm_hip_pack_a_dev(4, 100, None, None, None) == 1
+    # fused producers: prep_rows' shape rules, and gelu_mul needs up
+    fake = C.c_void_p(4096)
+    assert L.fgm_hip_prep_rmsnorm_dev(fake, 100, None, 1e-6, None, None, None, fake, fake, 4, 100,
+                                      0, None) == 1
+    assert L.fgm_hip_prep_rmsnorm_dev(fake, 64, None, 1e-6, None, None, None, fake, fake, -1, 64,
+                                      0, None) == 1
+    assert L.fgm_hip_prep_gelu_mul_dev(fake, None, 128, None, None, None, fake, fake, 4, 128, 0,
+                                       None) == 1
+    assert b"up is NULL" in L.fgm_hip_last_error()
 
 
 def test_no_gpu_means_no_backend():

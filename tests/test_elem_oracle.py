@@ -1,4 +1,4 @@
-"""The oracle's elementwise restatements (oracle/fgm_oracle.c, ops.c:17-142,
+"""The oracle's elementwise restatements (oracle/fgm_oracle.c, ops.c:15-147,
 316-350) pinned three ways:
 
 * byte-for-byte against the reference's own ops.c outputs recorded in
