@@ -57,9 +57,11 @@ FGM_DEV v16i mfma32(v4i a, v4i b, v16i c) {
 // Row position of weight-tile row r in the int8 LDS layout (an involution).
 FGM_DEV int rho(int r) { return (r & ~3) | ((r + 2 * ((r >> 2) & 1)) & 3); }
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW>
 struct Cfg {
-  static constexpr int NW = WGM * WGN, T = 64 * NW;
+  // KW groups of WGM x WGN waves; group g multiplies the k-blocks of stages
+  // g, g + KW, ... with a ring of its own (KW > 1: int8 only)
+  static constexpr int NWG = WGM * WGN, NW = NWG * KW, T = 64 * NW;
   static constexpr int BM = 32 * WMT * WGM, BN = 32 * WNT * WGN;
   static constexpr int MBL = BM / 16, NBL = BN / 16;
   static constexpr int BUNIT = BITS == 8 ? 1088 : 1024;     // LDS bytes per B unit
@@ -71,22 +73,29 @@ struct Cfg {
   static constexpr int STAGE = KS * KBLK;                     // KS k-blocks per ring slot
   // DMA instructions per wave per k-block (A units, B units, the int4
   // scales) and per stage
-  static constexpr int UK = (MBL + NW - 1) / NW + (BUNITS + NW - 1) / NW + (BITS == 4 ? 1 : 0);
+  static constexpr int UK = (MBL + NWG - 1) / NWG + (BUNITS + NWG - 1) / NWG + (BITS == 4 ? 1 : 0);
   static constexpr int U = KS * UK;
   static_assert((NS - 2) * U <= 63, "vmcnt range");
   // the ring, a 1 KB sink for the zero loads that keep the per-wave load
   // count fixed, the epilogue scales
-  static constexpr size_t TRASH = (size_t)NS * STAGE;
+  static constexpr size_t TRASH = (size_t)KW * NS * STAGE;
   static constexpr size_t LDS = TRASH + 1024 + (BM + (BN + 63) / 64 * 64) * 4;
   static_assert(BITS == 8 || NBL % 2 == 0, "int4 tiles come in n-block pairs");
+  static_assert(KW == 1 || BITS == 8, "K groups: int8 (exact int32 partial sums)");
+  // the groups' partial tiles are summed through the ring, one group at a
+  // time, once the stream is done
+  static_assert(KW == 1 || (size_t)BM * BN * 4 <= TRASH, "K-group reduction space");
+  static_assert(LDS <= 160 * 1024, "LDS per workgroup");
 };
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW, bool G1>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
-  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1>
+__global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt) {
+  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick(bt);
-  const int tid = threadIdx.x, w = wave_id(), l = tid & 63, h = l >> 5, l32 = l & 31;
+  const int tid = threadIdx.x, wv = wave_id(), l = tid & 63, h = l >> 5, l32 = l & 31;
+  // K group kg, wave w within it
+  const int kg = wv / C::NWG, w = wv - kg * C::NWG;
   const int wm = w % WGM, wn = w / WGM;
 
   const int M = a.M, N = a.N, KB = a.K >> 6;
@@ -111,7 +120,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   // ---- DMA plan: wave w issues A units w, w + NW, ..., B units likewise,
   // and wave 0 the int4 scale unit; slots past the unit count load zeros
   // (FGM_OOB), so every wave issues exactly U loads per stage
-  constexpr int UA = (C::MBL + C::NW - 1) / C::NW, UB = (C::BUNITS + C::NW - 1) / C::NW;
+  constexpr int UA = (C::MBL + C::NWG - 1) / C::NWG, UB = (C::BUNITS + C::NWG - 1) / C::NWG;
   constexpr int US = BITS == 4 ? 1 : 0;
   static_assert(UA + UB + US == C::UK, "unit plan");
   const v4i ra = rsrc_words(a.A, (uint32_t)MBtot * KB * 1024);
@@ -125,13 +134,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   constexpr uint32_t SINK = 0xFFFFFFFFu;
 #pragma unroll
   for (int i = 0; i < UA; i++) {
-    const int u = w + C::NW * i, mb = mb0 + u, row = l >> 2, q = (l & 3) ^ ((row >> 2) & 3);
+    const int u = w + C::NWG * i, mb = mb0 + u, row = l >> 2, q = (l & 3) ^ ((row >> 2) & 3);
     alds[i] = u < C::MBL ? u * 1024 : SINK;
     avoffs[i] = (u < C::MBL && mb < MBtot) ? (uint32_t)mb * KB * 1024 + row * 64 + 16 * q : FGM_OOB;
   }
 #pragma unroll
   for (int i = 0; i < UB; i++) {
-    const int u = w + C::NW * i;
+    const int u = w + C::NWG * i;
     blds[i] = u < C::BUNITS ? C::A_BYTES + u * C::BUNIT : SINK;
     bvoffs[i] = FGM_OOB;
     if (BITS == 8) {
@@ -149,12 +158,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   const uint32_t sink = lds0 + (uint32_t)C::TRASH;
-  // loads of k-block j of stage sidx (k-blocks KS*sidx ...) into ring slot
-  // `slot`; zeros past K, which land in k-blocks that are never multiplied
+  // this K group's ring
+  const uint32_t ring0 = lds0 + (uint32_t)(kg * NS * C::STAGE);
+  const char* const gring = smem + kg * NS * C::STAGE;
+  // loads of k-block j of the group's stage sidx (k-blocks KS * (KW * sidx +
+  // kg) ...) into ring slot `slot`; zeros past K, which land in k-blocks that
+  // are never multiplied
   auto issue_part = [&](int sidx, int slot, int j) {
-    const int kb = sidx * KS + j;
+    const int kb = (sidx * KW + kg) * KS + j;
     const bool live = kb < KB;
-    const uint32_t sb = lds0 + slot * C::STAGE + j * C::KBLK;
+    const uint32_t sb = ring0 + slot * C::STAGE + j * C::KBLK;
 #pragma unroll
     for (int i = 0; i < UA; i++)
       dma16(ra, alds[i] == SINK ? sink : sb + alds[i], live ? avoffs[i] : FGM_OOB, (uint32_t)kb * 1024);
@@ -185,7 +198,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
     const v4i rsb = rsrc_words(a.b_scale, NCB ? (uint32_t)nbend * 64 : 0u);
 #pragma unroll
     for (int i = 0; i < CH; i++) {
-      const int c = w + C::NW * i;
+      const int c = wv + C::NW * i;
       if (c < NCA)
         dma4(rsa, lds0 + (uint32_t)C::TRASH + 1024 + c * 256, (uint32_t)(mtile * C::BM + 64 * c + l) * 4, 0);
       else if (c < NCA + NCB)
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   __syncthreads();
   issue_part(NS - 1, NS - 1, 0);
   sfor<0, NG>([&](auto gc) {  // in group order, as the loop reads them
-    fetch_grp(std::integral_constant<int, 0>{}, gc, smem);
+    fetch_grp(std::integral_constant<int, 0>{}, gc, gring);
     __builtin_amdgcn_sched_barrier(0);
   });
 
@@ -330,25 +343,53 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   // U2 stages keep the register set of every k-block a constant; k-blocks
   // past K hold zeros.
   constexpr int U2 = KS % 2 == 0 ? 1 : 2;
-  const int NSTG = (KB + KS * U2 - 1) / (KS * U2) * U2;
+  const int NSTG = (KB + KS * KW * U2 - 1) / (KS * KW * U2) * U2;
   for (int sb = 0; sb < NSTG; sb += U2) {
     sfor<0, U2 * KS>([&](auto ic) {
       constexpr int i = decltype(ic)::value, u = i / KS, j = i % KS, cur = i & 1;
-      const int sidx = sb + u, kb = sidx * KS + j;
+      const int sidx = sb + u, kb = (sidx * KW + kg) * KS + j;
       const bool fresh = BITS == 4 && (kb % gk) == 0;
       if constexpr (j + 1 < KS) {
         mma(std::integral_constant<int, cur>{}, fresh, sidx - 1 + NS, (sidx + NS - 1) % NS, j + 1,
-            smem + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
+            gring + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
       } else {
         wait_vm<(NS - 2) * C::U>();
         __syncthreads();
         mma(std::integral_constant<int, cur>{}, fresh, sidx + NS, sidx % NS, 0,
-            smem + ((sidx + 1) % NS) * C::STAGE);
+            gring + ((sidx + 1) % NS) * C::STAGE);
       }
       drain(std::integral_constant<int, cur>{}, kb);
     });
   }
   wait_vm<0>();
+
+  // ---- K groups: group gg = 1 .. KW - 1 in turn parks its int32 tile in
+  // the ring and group 0 adds it (exact); group 0 runs the epilogue
+  if constexpr (KW > 1) {
+    int32_t* R = (int32_t*)smem;
+    auto at = [&](int x, int y, int r) { return (((w * WMT + x) * WNT + y) * 16 + r) * 64 + l; };
+    for (int gg = 1; gg < KW; gg++) {
+      __syncthreads();  // every group is done with its ring / the last sum is read
+      if (kg == gg) {
+#pragma unroll
+        for (int x = 0; x < WMT; x++)
+#pragma unroll
+          for (int y = 0; y < WNT; y++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) R[at(x, y, r)] = acc[x][y][r];
+      }
+      __syncthreads();
+      if (kg == 0) {
+#pragma unroll
+        for (int x = 0; x < WMT; x++)
+#pragma unroll
+          for (int y = 0; y < WNT; y++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[x][y][r] += R[at(x, y, r)];
+      }
+    }
+    if (kg > 0) return;
+  }
 
   // ---- epilogue: one buffer store per output; rows past M fall outside the
   // tile's buffer range, columns past n1 are masked
@@ -384,10 +425,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmBatch bt) {
   }
 }
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, bool RAW, bool G1>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1>
 hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
-  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS>;
-  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, RAW, G1>;
+  using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
+  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, RAW, G1>;
   static hipError_t attr =
       hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
   if (attr != hipSuccess) return attr;
@@ -407,13 +448,13 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
 
 // Variant: raw-accumulator dumps or scaled outputs; int4 with 64-wide groups
 // (a fresh accumulator every k-block) or the general group size.
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW = 1>
 hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
-  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, true, false>(b, st);
+  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, true, false>(b, st);
   bool g1 = BITS == 4;
   for (int i = 0; i < b.count; i++) g1 = g1 && b.p[i].group == 64;
-  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false, BITS == 4>(b, st)
-            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, false, false>(b, st);
+  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, BITS == 4>(b, st)
+            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false>(b, st);
 }
 
 // Workgroup tiles of a batch for a BM x BN tile.
@@ -439,13 +480,17 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
     }
   // Tile and ring, from measured sweeps on MI355X: the largest tile that
   // still puts a workgroup on (nearly) every CU; rings of NS slots of KS
-  // k-blocks.  Small problems (M = 256 projections) take 64 x 32 tiles with a
-  // deeper ring.
+  // k-blocks.  Small int8 problems (the M = 256 projections) split K over
+  // groups of waves inside the workgroup: a wave's loads are issued at a
+  // bounded rate (about 16 GB/s per wave from L2 on MI355X), so a small tile
+  // needs more waves streaming it, and each group walks a quarter or half of
+  // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256).
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
     if (tiles(in, 128, 128) >= 240) return launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
     if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
-    return launch_any<8, 1, 1, 2, 1, 4, 2>(in, st);
+    if (tiles(in, 64, 64) >= 160) return launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
+    return launch_any<8, 1, 1, 2, 1, 3, 2, 4>(in, st);
   }
   if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
   if (tiles(in, 128, 64) >= 240) return launch_any<4, 2, 1, 2, 2, 2, 2>(in, st);

@@ -263,6 +263,20 @@ def test_gpu_vs_reference_live(kind, M):
     assert _bits_equal(C, RC)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(256, 512, 8192), (256, 2560, 512), (200, 2048, 2048), (96, 1024, 4096)])
+def test_dense_k_groups_exact(M, N, Kd):
+    """Prefill-sized int8 GEMMs take the variants that split K over groups of
+    waves and add the groups' int32 tiles: the accumulators equal the exact
+    integer products and the scaled outputs the oracle's bytes."""
+    print("q8c", M, N, Kd, F_path("q8c", M, Kd, 0), flush=True)
+    A, Ap, a_s, B, bs = _inputs("q8c", M, N, Kd, 64, seed=4242 + M + N)
+    acc = H.gpu_acc("q8c", M, N, Kd, Ap, B)
+    assert np.array_equal(acc, H.exact_acc(A, H.decode_b8(B, N, Kd)))
+    C = H.gpu_gemm("q8c", M, N, Kd, Ap, a_s, B, bs)
+    R = _oracle("q8c", M, N, Kd, Ap, a_s, B, bs, 64, 0, N // 16)
+    assert _bits_equal(C, R)
+
+
 # ----------------------------------------------------------- batched calls
 @pytest.mark.parametrize("M", [8, 256])
 def test_batched_gemms_equal_single_calls(M):
