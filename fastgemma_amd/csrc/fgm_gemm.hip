@@ -457,6 +457,13 @@ hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
             : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false>(b, st);
 }
 
+// Shortest K of a batch.
+int kmin(const GemmBatch& b) {
+  int k = b.p[0].K;
+  for (int i = 1; i < b.count; i++) k = b.p[i].K < k ? b.p[i].K : k;
+  return k;
+}
+
 // Workgroup tiles of a batch for a BM x BN tile.
 long tiles(const GemmBatch& b, int bm, int bn) {
   long t = 0;
@@ -484,10 +491,13 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // groups of waves inside the workgroup: a wave's loads are issued at a
   // bounded rate (about 16 GB/s per wave from L2 on MI355X), so a small tile
   // needs more waves streaming it, and each group walks a quarter or half of
-  // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256).
+  // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256;
+  // M = 2048 down, K = 8192: 42.4 -> 38.9 us).
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
-    if (tiles(in, 128, 128) >= 240) return launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
+    if (tiles(in, 128, 128) >= 240)  // long K (the down projection): two K groups
+      return kmin(in) >= 4096 ? launch_any<8, 2, 2, 2, 2, 2, 2, 2>(in, st)
+                              : launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
     if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
     if (tiles(in, 64, 64) >= 160) return launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
     return launch_any<8, 1, 1, 2, 1, 3, 2, 4>(in, st);

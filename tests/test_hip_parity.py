@@ -277,6 +277,21 @@ def test_dense_k_groups_exact(M, N, Kd):
     assert _bits_equal(C, R)
 
 
+def test_dense_k_groups_large():
+    """M=2048, K=8192 int8 (the long-prefill down projection) takes 128x128
+    tiles with two K groups: exact accumulators, and the epilogue's bytes
+    recomputed from them as (float)acc * (b_scale * a_scale)."""
+    M, N, Kd = 2048, 2048, 8192
+    print("q8c", M, N, Kd, flush=True)
+    A, Ap, a_s, B, bs = _inputs("q8c", M, N, Kd, 64, seed=99)
+    acc = H.gpu_acc("q8c", M, N, Kd, Ap, B)
+    want = H.exact_acc(A, H.decode_b8(B, N, Kd))
+    assert np.array_equal(acc, want)
+    C = H.gpu_gemm("q8c", M, N, Kd, Ap, a_s, B, bs)
+    R = want.astype(np.float32) * (bs[None, :].astype(np.float32) * a_s[:, None].astype(np.float32))
+    assert _bits_equal(C, R.astype(np.float32))
+
+
 # ----------------------------------------------------------- batched calls
 @pytest.mark.parametrize("M", [8, 256])
 def test_batched_gemms_equal_single_calls(M):
