@@ -670,11 +670,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
                     help="run one extra measurement (cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
-                         "attn, model) and print its JSON instead of the headline line")
+                         "prep_fused, attn, model) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the N-sharded design is described in DESIGN.md); run with --gpus 1",
+              "(the weight stream would shard along N, one slice per GPU); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
