@@ -256,6 +256,22 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
 #pragma unroll
   for (int mb = 0; mb < MB; mb++) acc[mb] = v4i{0, 0, 0, 0};
   const int npro = min(D - 1, UPWw);             // units issued before PRE
+  // group 64: the chain reads the parked sums four k-tiles at a time, up to
+  // k-tile 4 ceil(KB / 4); the stream parks TR * UPW of them (zeros past K).
+  // When that is fewer (K of one or two k-tiles per round), the rest is set to
+  // zero here -- LDS left by an earlier workgroup may hold any bits, a NaN
+  // among them, and 0 * NaN would reach the output.  The barrier before the
+  // chain orders these writes.
+  if (BITS == 4 && G1 && !RAW) {
+    const int lo = TR * UPW, hi = ((KB + 3) >> 2) * 4;
+    if (hi > lo) {
+      float* Pz = (float*)(smem + L.park);
+      for (int i = tid; i < NBW * OUT * (hi - lo); i += NT) {
+        const int o = i / (hi - lo);
+        Pz[o * L.pp + lo + (i - o * (hi - lo))] = 0.0f;
+      }
+    }
+  }
 
   for (int u0 = 0; u0 < UPWw; u0 += D) {
     sfor<0, D>([&](auto ic) {
@@ -364,7 +380,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
         // past a row stay inside the workgroup's LDS and are not used.
         const uint32_t pa0 = lds0 + L.park + (uint32_t)((qq * OUT + oo) * L.pp) * 4u;
         const uint32_t sa0 = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
-        const int nch = (KB + 3) >> 2;           // k-tiles past K hold zeros
+        const int nch = (KB + 3) >> 2;           // k-tiles past K hold zeros (parked or set above)
         float cacc = 0.0f;
         v4i pv[4], sv[4];
         lds_read2x128<0>(pv[0], sv[0], pa0, sa0);

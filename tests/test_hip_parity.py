@@ -292,6 +292,22 @@ def test_dense_k_groups_large():
     assert _bits_equal(C, R.astype(np.float32))
 
 
+def test_group64_chain_ignores_stale_lds():
+    """int4 group 64 with K of one or two k-tiles: the fold reads its parked
+    sums four k-tiles at a time, past what the stream parks.  Run right after
+    a GEMM whose workgroups leave int32 partial sums in LDS (negative sums
+    read as float are NaN bit patterns): the outputs still equal the oracle."""
+    A, Ap, a_s, B, bs = _inputs("q8c", 256, 512, 2048, 64, seed=5)
+    H.gpu_gemm("q8c", 256, 512, 2048, Ap, a_s, B, bs)       # K-group reduction through LDS
+    for M in (1, 2, 8, 40, 64):
+        for Kd in (64, 128):
+            N = 64
+            A, Ap, a_s, B, bs = _inputs("q4g", M, N, Kd, 64, seed=300 + M + Kd)
+            C = H.gpu_gemm("q4g", M, N, Kd, Ap, a_s, B, bs, 64)
+            R = _oracle("q4g", M, N, Kd, Ap, a_s, B, bs, 64, 0, N // 16)
+            assert _bits_equal(C, R), (M, Kd)
+
+
 # ----------------------------------------------------------- batched calls
 @pytest.mark.parametrize("M", [8, 256])
 def test_batched_gemms_equal_single_calls(M):
