@@ -7,14 +7,16 @@
 // with the reference's operations in its order, so the bytes equal the two
 // separate calls'.
 //
-// One workgroup owns one activation row; each thread holds up to VMAX
-// consecutive float4s of it (vector i = thread + v * blockDim covers columns
-// 4i..4i+3) in registers from load to store.  With a rotation the row goes
-// through LDS once (every FWHT stage is one add or one subtract per element,
-// so the parallel schedule gives the reference's bytes).  The absolute
-// maximum is a wave reduction plus one LDS exchange (order-free for non-NaN
-// rows); then each float4 becomes one dword of the row-major int8 copy and
-// one dword of its packed tile.
+// One workgroup owns one activation row; each thread holds NV <= VMAX
+// float4s of it (vector i = thread + v * blockDim covers columns 4i..4i+3)
+// in registers from load to store, with the body compiled once per NV so
+// that no loop carries a bound check.  A rotation runs its stages of
+// distance 1 .. 128 in registers and across lanes and only longer ones
+// through LDS (every FWHT stage is one add or one subtract per element, so
+// the parallel schedule gives the reference's bytes).  The absolute maximum
+// is a wave reduction plus one LDS exchange (order-free for non-NaN rows);
+// then each float4 becomes one dword of the row-major int8 copy and one
+// dword of its packed tile.
 #include <algorithm>
 
 #include "fgm_common.h"
@@ -52,17 +54,27 @@ __device__ void fwht_lds(float* buf, int k, int hsz, float scale) {
   }
 }
 
-// The value lane ^ L of the wave holds (L < 64): DPP quad permutes for 1 and
-// 2, a row rotation for 8, ds_swizzle's xor mode (within 32 lanes) for 4 and
-// 16, ds_bpermute for 32.
+// One butterfly across lane distance L (< 64): the lane without bit L keeps
+// x + y, its partner (lane ^ L) keeps y - x, with y the other lane's value;
+// both are y + (+-x), the same single rounding.  A row of k = 8192 puts two
+// waves on each SIMD, so the stages are VALU-issue-bound and each costs two
+// VALU ops per value: the sign select and an add that reads y itself.  For 1,
+// 2 and 8 the exchange is a full-mask DPP pattern (quad permutes, a row
+// rotation) that folds into the add as v_add_f32_dpp; 4 and 16 use
+// ds_swizzle's xor mode (within 32 lanes) and 32 ds_bpermute, which run on
+// the LDS pipe.  (v_permlane16/32_swap need a register copy first and cost
+// one more VALU op than the LDS forms.)
 template <int L>
-__device__ __forceinline__ float lane_xor(float v) {
-  const int b = __float_as_int(v);
-  if constexpr (L == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
-  else if constexpr (L == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
-  else if constexpr (L == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
-  else if constexpr (L < 32) return __int_as_float(__builtin_amdgcn_ds_swizzle(b, (L << 10) | 0x1F));
-  else return __shfl_xor(v, L, 64);
+__device__ __forceinline__ float butterfly(float x, bool upper) {
+  const float s = upper ? -x : x;
+  const int b = __float_as_int(x);
+  int p;
+  if constexpr (L == 1) p = __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, true);
+  else if constexpr (L == 2) p = __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, true);
+  else if constexpr (L == 8) p = __builtin_amdgcn_update_dpp(0, b, 0x128, 0xF, 0xF, true);
+  else if constexpr (L < 32) p = __builtin_amdgcn_ds_swizzle(b, (L << 10) | 0x1F);
+  else p = __float_as_int(__shfl_xor(x, L, 64));
+  return __int_as_float(p) + s;
 }
 
 // Maximum over the 64 lanes of a wave: DPP within each 16-lane row, then the
@@ -99,42 +111,24 @@ __device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
   return p;
 }
 
-template <int PRE>
-__global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
-  extern __shared__ float buf[];
-  __shared__ float red[PREP_MAX_THREADS / 64];
-  const PrepProb a = pick(bt);
-  const int row = a.r0 + (blockIdx.x - a.wg0);
+// The computing part of prep_rows_kernel for a row whose float4s fit NV per
+// thread (4 T NV >= k).  Every per-float4 loop is fully unrolled with no
+// bound checks: float4s past the row read 0 through the buffer range check,
+// stay 0 through every stage (the rotation's blocks past k hold only them),
+// do not move the maximum, and their stores fall outside the store ranges.
+template <int PRE, int NV>
+__device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf, float* red) {
   const int k = a.k, KB = k >> 6;
   const int T = blockDim.x, tid = threadIdx.x;
 
-  if (row >= a.r1) {
-    // Rows of the last covered tile block beyond r1: zero padding when past m,
-    // otherwise whatever the caller's qa row holds (ops.c:308-311).
-    if (!a.pa) return;
-    for (int c = tid * 4; c < k; c += T * 4) {
-      int32_t v = 0;
-      if (row < a.m) {
-        const int8_t* q = a.qa + (size_t)row * k + c;
-        v = (int32_t)((uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
-                      (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24);
-      }
-      *(int32_t*)(a.pa + pa_off(row, c, KB)) = v;
-    }
-    return;
-  }
-
-  // 1. the row into registers; lanes past its end read 0 (buffer range check)
+  // 1. the row into registers
   const float* src = a.src + (size_t)row * a.lda;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)k * 4);
   const bool vec = ((((uintptr_t)a.src) & 15) == 0) && (a.lda & 3) == 0 && (k & 3) == 0;
-  // float4s per thread that reach into the row (uniform)
-  const int nv = ((k + 3) / 4 + T - 1) / T;
-  float x[VMAX][4];
+  float x[NV][4];
   if (vec) {
 #pragma unroll
-    for (int v = 0; v < VMAX; v++) {
-      if (v >= nv) break;
+    for (int v = 0; v < NV; v++) {
       const int c = 4 * (tid + v * T);
       const v4i q = buf_load_b128(rs, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
 #pragma unroll
@@ -142,8 +136,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     }
   } else {
 #pragma unroll
-    for (int v = 0; v < VMAX; v++) {
-      if (v >= nv) break;
+    for (int v = 0; v < NV; v++) {
       const int c = 4 * (tid + v * T);
 #pragma unroll
       for (int e = 0; e < 4; e++)
@@ -155,13 +148,12 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   //     cover the whole row, no scalar tails)
   if constexpr (PRE == PREP_RMSNORM) {
     // w is loaded before the reduction so its latency hides behind it
-    float w[VMAX][4];
+    float w[NV][4];
     if (a.aux) {
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.aux, (uint32_t)k * 4);
       const bool wvec = (((uintptr_t)a.aux) & 15) == 0;
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
         if (wvec) {
           const v4i q = buf_load_b128(rw, c < k ? (uint32_t)c * 4 : FGM_OOB, 0);
@@ -180,8 +172,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     const int S = fgm_rms_stride(k);
     auto tpos = [&](int i4) { return buf + 4 * (i4 & 3) * S + (i4 >> 2); };
 #pragma unroll
-    for (int v = 0; v < VMAX; v++) {
-      if (v >= nv) break;
+    for (int v = 0; v < NV; v++) {
       const int i4 = tid + v * T;
       if (4 * i4 < k) {
         float* p = tpos(i4);
@@ -200,8 +191,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     // reduction (w and the chains' read-ahead already need them).
     const float rinv = buf[16 * S];
 #pragma unroll
-    for (int v = 0; v < VMAX; v++) {
-      if (v >= nv) break;
+    for (int v = 0; v < NV; v++) {
       const int i4 = tid + v * T;
       const float* p = tpos(i4);
 #pragma unroll
@@ -215,8 +205,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.aux + (size_t)row * a.lda, (uint32_t)k * 4);
     const bool uvec = ((((uintptr_t)a.aux) & 15) == 0) && (a.lda & 3) == 0;
 #pragma unroll
-    for (int v = 0; v < VMAX; v++) {
-      if (v >= nv) break;
+    for (int v = 0; v < NV; v++) {
       const int c = 4 * (tid + v * T);
       float u[4];
       if (uvec) {
@@ -234,18 +223,21 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   }
   if constexpr (PRE != PREP_COPY) {
     if (a.pre) {
-      float* o = a.pre + (size_t)row * k;
+      const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.pre + (size_t)row * k, (uint32_t)k * 4);
       const bool ovec = (((uintptr_t)a.pre) & 15) == 0;
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
-        if (c >= k) break;
+        const uint32_t off = c < k ? (uint32_t)c * 4 : FGM_OOB;
         if (ovec) {
-          *(float4*)(o + c) = make_float4(x[v][0], x[v][1], x[v][2], x[v][3]);
+          const v4i q = {__float_as_int(x[v][0]), __float_as_int(x[v][1]), __float_as_int(x[v][2]),
+                         __float_as_int(x[v][3])};
+          __builtin_amdgcn_raw_buffer_store_b128(q, ro, off, 0, 0);
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; e++) o[c + e] = x[v][e];
+          for (int e = 0; e < 4; e++)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[v][e]), ro,
+                                                  c < k ? off + 4 * e : FGM_OOB, 0, 0);
         }
       }
     }
@@ -262,16 +254,14 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     const int lane = tid & 63;
     if (hsz > 1) {
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const float u0 = x[v][0], u1 = x[v][1], u2 = x[v][2], u3 = x[v][3];
         x[v][0] = u0 + u1, x[v][1] = u0 - u1, x[v][2] = u2 + u3, x[v][3] = u2 - u3;
       }
     }
     if (hsz > 2) {
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const float u0 = x[v][0], u1 = x[v][1], u2 = x[v][2], u3 = x[v][3];
         x[v][0] = u0 + u2, x[v][1] = u1 + u3, x[v][2] = u0 - u2, x[v][3] = u1 - u3;
       }
@@ -281,21 +271,15 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
       if (hsz > 4 * L) {
         const bool upper = lane & L;
 #pragma unroll
-        for (int v = 0; v < VMAX; v++) {
-          if (v >= nv) break;
+        for (int v = 0; v < NV; v++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const float y = lane_xor<L>(x[v][e]);
-            x[v][e] = upper ? y - x[v][e] : x[v][e] + y;
-          }
-        }
+          for (int e = 0; e < 4; e++) x[v][e] = butterfly<L>(x[v][e], upper);
       }
     });
     if (hsz > 256) {
       if constexpr (PRE == PREP_RMSNORM) __syncthreads();  // x was re-read from buf
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
 #pragma unroll
         for (int e = 0; e < 4; e++)
@@ -304,8 +288,7 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
       __syncthreads();
       fwht_lds_stages(buf, k, hsz, 8);
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
 #pragma unroll
         for (int e = 0; e < 4; e++) x[v][e] = (c + e < k) ? buf[c + e] : 0.0f;
@@ -313,22 +296,18 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     }
     if (hsz >= 16) {
 #pragma unroll
-      for (int v = 0; v < VMAX; v++) {
-        if (v >= nv) break;
+      for (int v = 0; v < NV; v++)
 #pragma unroll
         for (int e = 0; e < 4; e++) x[v][e] = x[v][e] * a.fwht_scale;
-      }
     }
   }
 
   // 3. absolute maximum of the row
   float mx = 0.0f;
 #pragma unroll
-  for (int v = 0; v < VMAX; v++) {
-    if (v >= nv) break;
+  for (int v = 0; v < NV; v++)
 #pragma unroll
     for (int e = 0; e < 4; e++) mx = fmaxf(mx, __builtin_fabsf(x[v][e]));
-  }
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
@@ -340,13 +319,43 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
 
   // 4. quantise and store: vector part [0, k & ~15) as _mm512_cvtps_epi32 +
   //    saturation, the scalar tail as lrintf + clamp (ops.c:194-203)
+  if ((k & 15) == 0) {
+    // the whole row in vector form: one dword of int8 per float4, stores
+    // past the row dropped by the range check.  The packed tile row of
+    // `row` is 64 bytes every 1024: [row/16][k/64][row%16][k%64].
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(a.rot ? a.rot + (size_t)row * k : nullptr, a.rot ? (uint32_t)k * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(a.qa ? a.qa + (size_t)row * k : nullptr, a.qa ? (uint32_t)k : 0);
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(a.pa ? a.pa + ((size_t)(row >> 4) * KB * 16 + (row & 15)) * 64 : nullptr,
+                  a.pa ? (uint32_t)KB * 1024 : 0);
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int c = 4 * (tid + v * T);
+      const bool in = c < k;
+      const uint32_t packed =
+          pack4_i8(quant_vec_i(x[v][0] * inv), quant_vec_i(x[v][1] * inv),
+                   quant_vec_i(x[v][2] * inv), quant_vec_i(x[v][3] * inv));
+      if (a.rot) {
+        const v4i q = {__float_as_int(x[v][0]), __float_as_int(x[v][1]), __float_as_int(x[v][2]),
+                       __float_as_int(x[v][3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, rr, in ? (uint32_t)c * 4 : FGM_OOB, 0, 0);
+      }
+      if (a.qa)
+        __builtin_amdgcn_raw_buffer_store_b32((int)packed, rq, in ? (uint32_t)c : FGM_OOB, 0, 0);
+      if (a.pa)
+        __builtin_amdgcn_raw_buffer_store_b32(
+            (int)packed, rp, in ? (uint32_t)((c >> 6) * 1024 + (c & 63)) : FGM_OOB, 0, 0);
+    }
+    return;
+  }
   const int kv = k & ~15;
   float* rot = a.rot ? a.rot + (size_t)row * k : nullptr;
   int8_t* qa = a.qa ? a.qa + (size_t)row * k : nullptr;
   const bool dw = (k & 3) == 0;  // rows of qa / rot start 4-byte aligned
 #pragma unroll
-  for (int v = 0; v < VMAX; v++) {
-    if (v >= nv) break;
+  for (int v = 0; v < NV; v++) {
     const int c = 4 * (tid + v * T);
     if (c >= k) break;
     uint32_t packed;
@@ -375,6 +384,38 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     }
     if (a.pa) *(uint32_t*)(a.pa + pa_off(row, c, KB)) = packed;
   }
+}
+
+template <int PRE>
+__global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
+  extern __shared__ float buf[];
+  __shared__ float red[PREP_MAX_THREADS / 64];
+  const PrepProb a = pick(bt);
+  const int row = a.r0 + (blockIdx.x - a.wg0);
+  const int k = a.k, KB = k >> 6;
+  const int T = blockDim.x, tid = threadIdx.x;
+
+  if (row >= a.r1) {
+    // Rows of the last covered tile block beyond r1: zero padding when past m,
+    // otherwise whatever the caller's qa row holds (ops.c:308-311).
+    if (!a.pa) return;
+    for (int c = tid * 4; c < k; c += T * 4) {
+      int32_t v = 0;
+      if (row < a.m) {
+        const int8_t* q = a.qa + (size_t)row * k + c;
+        v = (int32_t)((uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
+                      (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24);
+      }
+      *(int32_t*)(a.pa + pa_off(row, c, KB)) = v;
+    }
+    return;
+  }
+  // float4s per thread that reach into the row (uniform; the launcher keeps
+  // it within 1 .. VMAX)
+  const int nv = ((k + 3) / 4 + T - 1) / T;
+  sfor<1, VMAX + 1>([&](auto N) {
+    if (nv == N) prep_row<PRE, N>(a, row, buf, red);
+  });
 }
 
 // fgm_pack_a (ops.c:279-290), 16 bytes per thread.
