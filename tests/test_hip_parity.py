@@ -193,7 +193,7 @@ def test_pack_a_matches_oracle():
 def test_quant_heavy_tails_and_odd_lengths_vs_oracle():
     from fastgemma_amd import kernels
     t = H.torch()
-    for rows, k in ((64, 2048), (9, 8192), (3, 100), (5, 16), (2, 1)):
+    for rows, k in ((64, 2048), (9, 8192), (3, 100), (5, 16), (2, 1), (3, 6150), (2, 16376)):
         x = oracle.gen_student_t(rows * 7 + k, rows * k, 3).reshape(rows, k)
         x[:, :: max(1, k // 3)] *= 20.0
         q = t.empty((rows, k), dtype=t.int8, device="cuda")

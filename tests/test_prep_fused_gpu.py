@@ -22,10 +22,16 @@ EPS = 1e-6
 
 # (m, k, hsz, lda): decode and prefill rows of the model's widths, a rotation
 # per case, a padded row stride, the largest k a row of LDS holds
+# per-row float4s per thread (the row body is compiled once per count, 1 ..
+# 8): 512 threads per row up to k = 2048 * 8 for rmsnorm, 1024 for gelu_mul;
+# the cases below reach every count for both producers
 RMS_CASES = [(1, 2560, 0, 2560), (8, 2560, 256, 2560), (13, 1536, 512, 1600),
-             (37, 5376, 0, 5376), (3, 32768, 1024, 32768), (16, 64, 64, 64), (100, 3840, 128, 3840)]
+             (37, 5376, 0, 5376), (3, 32768, 1024, 32768), (16, 64, 64, 64), (100, 3840, 128, 3840),
+             (3, 8192, 128, 8192), (2, 10240, 0, 10240), (2, 12288, 512, 12352),
+             (2, 14336, 128, 14336)]
 GELU_CASES = [(8, 10240, 0, 10240), (5, 16384, 1024, 16384), (20, 6144, 512, 6400),
-              (2, 32768, 0, 32768), (33, 2048, 2048, 2048)]
+              (2, 32768, 0, 32768), (33, 2048, 2048, 2048), (2, 20480, 128, 20480),
+              (2, 24576, 0, 24576), (2, 28672, 512, 28736)]
 
 
 def bits(a):
@@ -136,7 +142,8 @@ def test_fused_rejects_bad_shapes():
 
 
 ROT_CASES = [(5, 8192, h) for h in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192)] + \
-            [(3, 2560, h) for h in (4, 32, 256, 512)] + [(17, 192, 64), (2, 32768, 32768)]
+            [(3, 2560, h) for h in (4, 32, 256, 512)] + [(17, 192, 64), (2, 32768, 32768)] + \
+            [(3, 6144, 128), (2, 10240, 256), (2, 12288, 64), (2, 14336, 128), (2, 16384, 1024)]
 
 
 @pytest.mark.parametrize("case", ROT_CASES, ids=[f"m{c[0]}_k{c[1]}_h{c[2]}" for c in ROT_CASES])
