@@ -499,6 +499,8 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
   int threads = std::min(cap, ((kmax + 3) / 4 + 63) / 64 * 64);
   threads = std::max(threads, ((kmax + 4 * VMAX - 1) / (4 * VMAX) + 63) / 64 * 64);
   threads = std::max(64, std::min(threads, PREP_MAX_THREADS));
+  // the kernel has a row body for 1 .. VMAX float4s per thread only
+  if (((kmax + 3) / 4 + threads - 1) / threads > VMAX) return hipErrorInvalidValue;
   const size_t lds = (size_t)lds_floats * sizeof(float);
   if (pre == PREP_RMSNORM)
     hipLaunchKernelGGL(prep_rows_kernel<PREP_RMSNORM>, dim3(nwg), dim3(threads), lds, st, b);
