@@ -350,3 +350,30 @@ def test_batched_prep_equals_single_calls():
         assert np.array_equal(H.host(p["qa"]), rq)
         assert _bits_equal(H.host(p["qs"]), rs)
         assert np.array_equal(H.host(p["pa"]), rap)
+
+
+def test_batched_prep_wide_and_narrow_rows():
+    """One launch sizes its workgroups for the widest row (32768 columns:
+    1024 threads), so a 64-column row leaves whole waves past its end and a
+    6144-column one runs with two float4s per thread; rotations through
+    lanes and through LDS, every output requested, against the oracle."""
+    from fastgemma_amd import kernels
+    t = H.torch()
+    probs, refs = [], []
+    for i, (m, k, hsz) in enumerate([(3, 32768, 1024), (5, 64, 64), (2, 6144, 512)]):
+        x = (oracle.gen_student_t(90 + i, m * k, 3) * 2.0).reshape(m, k)
+        rot = t.full((m, k), 7.0, device="cuda")
+        qa = t.full((m, k), 5, dtype=t.int8, device="cuda")
+        qs = t.full((m,), 7.0, device="cuda")
+        pa = t.full((oracle.packed_a_len(m, k),), 5, dtype=t.int8, device="cuda")
+        probs.append(dict(src=H.dev(x), lda=k, rot=rot, qa=qa, qs=qs, pa=pa, m=m, k=k, hsz=hsz,
+                          r0=0, r1=m))
+        want = (np.zeros((m, k), np.float32), np.zeros((m, k), np.int8), np.zeros(m, np.float32),
+                np.zeros(oracle.packed_a_len(m, k), np.int8))
+        oracle.prep_rows(np.ascontiguousarray(x, np.float32), k, *want, m, k, hsz, 0, m)
+        refs.append(want)
+    kernels.prep_batch(probs)
+    for p, want in zip(probs, refs):
+        for name, w in zip(("rot", "qa", "qs", "pa"), want):
+            assert np.array_equal(H.host(p[name]).view(np.uint8), np.ascontiguousarray(w).view(np.uint8)), \
+                (p["k"], name)
