@@ -9,6 +9,7 @@
 //   they print the message and abort on failure.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -74,6 +75,28 @@ int ensure_device() {
 // One activation row (f32) is staged whole in LDS by the preamble kernels.
 constexpr size_t ROW_LDS_LIMIT = 128 * 1024;
 
+// The kernels address packed A, B and the scales through buffer descriptors
+// with 32-bit byte ranges and mask lanes with the offset FGM_OOB = 2^31, so a
+// launch's ranges must stay below 2^31 bytes.  B is cut along N into launches
+// of at most FGM_B_CHUNK bytes (the n-block range is contiguous in B, so a cut
+// is a rebased pointer); packed A and the int4 scale table cannot be cut that
+// way and are refused past the limit.
+constexpr uint64_t FGM_B_CHUNK = 1ull << 30;
+constexpr uint64_t FGM_RANGE_MAX = 1ull << 31;
+
+int check_ranges(int bits, int m, int n, int k, int group) {
+  const uint64_t abytes = (uint64_t)((m + 15) / 16) * 16 * (uint64_t)k;
+  if (abytes >= FGM_RANGE_MAX)
+    return fail(FGM_HIP_EINVAL, "gemm: packed A of %llu bytes (m=%d k=%d) reaches 2^31", (unsigned long long)abytes,
+                m, k);
+  if (bits == 4 && group > 0) {
+    const uint64_t sbytes = (uint64_t)(k / group) * (uint64_t)n * 2;
+    if (sbytes >= FGM_RANGE_MAX)
+      return fail(FGM_HIP_EINVAL, "gemm: int4 scale table of %llu bytes reaches 2^31", (unsigned long long)sbytes);
+  }
+  return FGM_HIP_OK;
+}
+
 // ---------------------------------------------------------- validation
 int check_gemm(int m, int n, int k, int ldc, int n0, int n1, int bits, int group) {
   if (m < 0 || n < 0 || k < 0) return fail(FGM_HIP_EINVAL, "negative shape m=%d n=%d k=%d", m, n, k);
@@ -87,7 +110,7 @@ int check_gemm(int m, int n, int k, int ldc, int n0, int n1, int bits, int group
     if (group <= 0 || group % 64 || k % group)
       return fail(FGM_HIP_EINVAL, "group=%d must be a multiple of 64 dividing k=%d", group, k);
   }
-  return FGM_HIP_OK;
+  return check_ranges(bits, m, n, k, group);
 }
 
 // Skinny kernel for m <= 64 when its LDS fits, else the dense MFMA kernel.
@@ -121,6 +144,32 @@ GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, c
 // Launch validated problems of one weight type: skinny ones share launches,
 // dense ones share launches, FGM_MAX_BATCH per launch.  Empty problems are
 // skipped; an empty contraction (k == 0) writes 0, as the reference does.
+int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st);
+
+// One problem whose B spans more than FGM_B_CHUNK bytes, as launches over
+// n-block chunks: B, the scales' column, C and acc_out are rebased to the
+// chunk's first column; N stays the scale table's row stride.
+int run_chunked(int bits, const GemmProb& p, hipStream_t st) {
+  const uint64_t nb_bytes = (uint64_t)p.K * (bits == 8 ? 16 : 8);
+  int step = (int)std::min<uint64_t>(FGM_B_CHUNK / nb_bytes, 1u << 24);
+  if (step < 1) step = 1;  // one n-block of K * 16 bytes: K < 2^27, as packed A's limit implies
+  for (int c0 = p.n0; c0 < p.n0 + p.nblocks; c0 += step) {
+    GemmProb q = p;
+    const int cnt = std::min(step, p.n0 + p.nblocks - c0);
+    q.B = (const int8_t*)p.B + (size_t)c0 * nb_bytes;
+    if (p.b_scale)
+      q.b_scale = bits == 8 ? (const void*)((const float*)p.b_scale + 16 * (size_t)c0)
+                            : (const void*)((const uint16_t*)p.b_scale + 16 * (size_t)c0);
+    if (p.C) q.C = p.C + 16 * (size_t)c0;
+    if (p.acc_out) q.acc_out = p.acc_out + 16 * (size_t)c0;
+    q.n0 = 0;
+    q.nblocks = cnt;
+    int rc = run_probs(bits, &q, 1, st);
+    if (rc) return rc;
+  }
+  return FGM_HIP_OK;
+}
+
 int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
   GemmBatch sk{}, de{};
   auto flush = [&](GemmBatch& b, int dense) -> int {
@@ -139,9 +188,16 @@ int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
     if (p.K > 0 && !p.acc_out && (!p.a_scale || !p.b_scale))
       return fail(FGM_HIP_EINVAL, "gemm: a_scale or b_scale is NULL");
     if (p.K == 0) {
-      if (!p.acc_out)
-        HIPCHK(hipMemset2DAsync(p.C + 16 * p.n0, (size_t)p.ldc * 4, 0, (size_t)p.nblocks * 64,
-                                p.M, st));
+      // a fill kernel, not a memset: this path may be captured into a graph
+      if (!p.acc_out) {
+        hipError_t e = fgm_launch_fill_zero(p.C + 16 * p.n0, p.ldc, p.M, 16 * p.nblocks, st);
+        if (e != hipSuccess) return hip_fail(e, "zero fill launch");
+      }
+      continue;
+    }
+    int rc;
+    if ((uint64_t)(p.n0 + p.nblocks) * (uint64_t)p.K * (bits == 8 ? 16 : 8) > FGM_B_CHUNK) {
+      if ((rc = run_chunked(bits, p, st))) return rc;
       continue;
     }
     const int dense = gemm_path(bits, p.M, p.K, p.group);
@@ -194,6 +250,10 @@ struct CachedBuf {
 struct WeightCache {
   std::shared_mutex mu;
   std::unordered_map<const void*, CachedBuf> map;
+  // copies replaced after a fingerprint mismatch: another thread may have
+  // been handed the old device pointer and still be launching on it, so it
+  // is freed only by fgm_hip_weight_cache_clear()
+  std::vector<void*> retired;
 } g_wcache;
 
 uint64_t fingerprint(const void* host, size_t bytes) {
@@ -225,7 +285,7 @@ int cached_upload(const void* host, size_t bytes, void** dev) {
       *dev = it->second.dev;
       return FGM_HIP_OK;
     }
-    HIPCHK(hipFree(it->second.dev));
+    g_wcache.retired.push_back(it->second.dev);
     g_wcache.map.erase(it);
   }
   void* d = nullptr;
@@ -506,8 +566,13 @@ int fgm_hip_fwht_dev(float* x, int n, int hsz, void* stream) {
 // ---------------------------------------------------------------- drop-ins
 void fgm_hip_weight_cache_clear(void) {
   std::unique_lock<std::shared_mutex> lk(g_wcache.mu);
+  // callers clear the cache when no drop-in call is in flight; the device is
+  // synchronised so that no queued kernel still reads a freed copy
+  (void)hipDeviceSynchronize();
   for (auto& kv : g_wcache.map) (void)hipFree(kv.second.dev);
+  for (void* d : g_wcache.retired) (void)hipFree(d);
   g_wcache.map.clear();
+  g_wcache.retired.clear();
 }
 
 void fgm_gemm_q8c_hip(int m, int n, int k, const int8_t* a, const float* a_scale, const int8_t* b,

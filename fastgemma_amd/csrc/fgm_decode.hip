@@ -73,6 +73,7 @@ constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thre
 #define FGM_DEC_NWMIN 4           // smallest number of stream waves per workgroup
 #endif
 
+static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
 FGM_DEV GemmProb pick(const GemmBatch& bt) {
   const int b = blockIdx.x;
   GemmProb p = bt.p[0];

@@ -168,9 +168,22 @@ __global__ __launch_bounds__(256) void binop_kernel(float* a, const float* b, in
   else a[i] = a[i] * s;
 }
 
+// zeros into rows x cols floats, rows ld apart (an empty contraction's C)
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int ld, int cols) {
+  float* row = p + (size_t)blockIdx.y * ld;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < cols; i += gridDim.x * blockDim.x) row[i] = 0.0f;
+}
+
 unsigned blocks(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
+
+hipError_t fgm_launch_fill_zero(float* p, int ld, int rows, int cols, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  const unsigned gx = std::min(blocks(cols), 64u);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(gx, rows), dim3(256), 0, st, p, ld, cols);
+  return hipGetLastError();
+}
 
 hipError_t fgm_launch_rmsnorm(float* out, const float* x, const float* w, int rows, int n, float eps,
                               hipStream_t st) {

@@ -41,6 +41,7 @@ namespace {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
 FGM_DEV GemmProb pick(const GemmBatch& bt) {
   const int b = blockIdx.x;
   GemmProb p = bt.p[0];

@@ -6,7 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
-// Independent problems served by one launch.
+// Independent problems served by one launch.  The kernels' pick() selects a
+// problem with four unrolled comparisons; it asserts this value.
 constexpr int FGM_MAX_BATCH = 4;
 
 struct GemmProb {
@@ -78,6 +79,8 @@ hipError_t fgm_launch_gelu(float* out, const float* gate, const float* up, int n
 hipError_t fgm_launch_softcap(float* x, int n, float cap, hipStream_t st);
 hipError_t fgm_launch_rope(float* x, int rows, int n_heads, int head_dim, const float* cs, hipStream_t st);
 hipError_t fgm_launch_binop(float* a, const float* b, int n, int op, float s, hipStream_t st);
+// zeros into rows x cols floats with row stride ld (no memset node in a graph)
+hipError_t fgm_launch_fill_zero(float* p, int ld, int rows, int cols, hipStream_t st);
 
 // int8-KV attention (fgm_attn.hip).  Rows are grouped into sequences: rows
 // [row0, row0 + nrows) of one sequence read one layer cache and sit at

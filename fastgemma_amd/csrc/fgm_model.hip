@@ -398,11 +398,30 @@ int linear_of(const fgm_hip_model* m, const char* name, fgm_hip_linear* o) {
   const std::string sname = std::string(name) + ".scale";
   const Tensor* s = find(m, sname.c_str());
   if (!s) return fail(FGM_HIP_EINVAL, "model: missing tensor %s", sname.c_str());
+  // the GEMM reads n * k (int8) or n * k / 2 (int4) weight bytes and the
+  // scales' n (f32) or (k / group) * n (f16) entries: a short or malformed
+  // tensor is refused here rather than read past its end on the device
+  const int64_t n = t->shape[0], k = t->shape[1];
+  const int group = bits == 4 ? (t->group >= 0 ? t->group : 64) : 0;
+  if (n <= 0 || k <= 0 || n % 16 || k % 64 || n > 0x7fffffff || k > 0x7fffffff)
+    return fail(FGM_HIP_EINVAL, "model: %s has shape [%lld, %lld] (n %% 16 == 0, k %% 64 == 0 required)", name,
+                (long long)n, (long long)k);
+  if (bits == 4 && (group <= 0 || group % 64 || k % group))
+    return fail(FGM_HIP_EINVAL, "model: %s has group %d (a multiple of 64 dividing k=%lld required)", name, group,
+                (long long)k);
+  const uint64_t wbytes = bits == 8 ? (uint64_t)n * k : (uint64_t)n * k / 2;
+  const uint64_t sbytes = bits == 8 ? (uint64_t)n * 4 : (uint64_t)(k / group) * n * 2;
+  if (t->nbytes < wbytes)
+    return fail(FGM_HIP_EINVAL, "model: %s holds %zu bytes, its shape needs %llu", name, t->nbytes,
+                (unsigned long long)wbytes);
+  if (s->nbytes < sbytes)
+    return fail(FGM_HIP_EINVAL, "model: %s holds %zu bytes, %s needs %llu", sname.c_str(), s->nbytes, name,
+                (unsigned long long)sbytes);
   memset(o, 0, sizeof *o);
   o->bits = bits;
-  o->n = (int)t->shape[0];
-  o->k = (int)t->shape[1];
-  o->group = bits == 4 ? (t->group >= 0 ? t->group : 64) : 0;
+  o->n = (int)n;
+  o->k = (int)k;
+  o->group = group;
   o->hadamard = t->hadamard;
   o->b_host = m->host(*t);
   o->b_scale_host = m->host(*s);

@@ -102,6 +102,7 @@ __device__ __forceinline__ size_t pa_off(int row, int col, int KB) {
 
 // The problem a workgroup belongs to, chosen with uniform selects so the
 // kernel-argument array is never indexed dynamically.
+static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
 __device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
   const int b = blockIdx.x;
   PrepProb p = bt.p[0];

@@ -107,6 +107,25 @@ def lib() -> C.CDLL:
     return _LIB
 
 
+class fault:
+    """Context manager that makes the oracle compute one deliberately wrong
+    variant (see the orc_fault table in fgm_oracle.c), for negative controls:
+    ``with oracle.fault(1): ...``.  Test infrastructure only."""
+
+    def __init__(self, kind: int):
+        self.kind = kind
+
+    def __enter__(self):
+        v = C.c_int.in_dll(lib(), "orc_fault")
+        self.prev = v.value
+        v.value = self.kind
+        return self
+
+    def __exit__(self, *exc):
+        C.c_int.in_dll(lib(), "orc_fault").value = self.prev
+        return False
+
+
 def _bind_ref(L: C.CDLL) -> None:
     L.fgm_cpu_has_amx.restype = _i
     L.fgm_cpu_has_avx512_vnni.restype = _i

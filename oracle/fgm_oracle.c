@@ -34,6 +34,23 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* ------------------------------------------------------- fault injection
+ * Negative controls for the parity checks (tests/test_negative_controls.py):
+ * a non-zero orc_fault makes the oracle compute one plausible WRONG variant,
+ * so the tests can show that the golden / reference byte comparisons reject
+ * it.  Each variant is a neighbouring convention the reference itself
+ * contains or once contained:
+ *   1  q8c epilogue (float)acc * as * bs           (vnni_test.c:72-85's ref_q8c)
+ *   2  q8c per-64-k-tile float sums, then *= as*bs (amx_gemm.c:500-522)
+ *   3  int4 nibble as offset binary, v - 8         (JOURNAL.md:1908-1937)
+ *   4  q4g unfused C = (float)acc * s + C          (amx_gemm.c:478-498)
+ *   5  q4g groups summed in descending order
+ *   6  quant_act truncating instead of rounding to nearest even
+ *   10 attention softmax sum as one serial chain instead of 16 lane sums
+ *   11 attention P.V counting a slot shared by two ring spans once
+ * 0 (the default) is the reference's behaviour; nothing else reads it. */
+int orc_fault = 0;
+
 /* ------------------------------------------------------------ f16 helpers */
 
 /* Exact IEEE binary16 -> binary32 widening (every half value is exactly
@@ -97,7 +114,7 @@ uint16_t orc_f32_to_f16(float f) {
  * an out-of-range value gives the "integer indefinite" 0x80000000. */
 static int32_t cvt_ps_epi32_rne(float v) {
   if (!(fabsf(v) < 2147483648.0f)) return INT32_MIN;
-  return (int32_t)rintf(v);
+  return orc_fault == 6 ? (int32_t)v : (int32_t)rintf(v);
 }
 
 /* _mm512_cvtsepi32_epi8: signed saturation to [-128, 127]. */
@@ -221,7 +238,7 @@ static inline int b4_val(const uint8_t *Bq, int K, int k, int n) {
   size_t blk = p / 64, off = p % 64;
   uint8_t byte = Bq[blk * 32 + off % 32];
   int v = (off < 32) ? (byte & 0xF) : (byte >> 4);
-  return (v ^ 8) - 8;
+  return orc_fault == 3 ? v - 8 : (v ^ 8) - 8;
 }
 
 /* pack_b_tiles, quant.py:96-107: q[N][K] row-major (out, in) -> tile stream. */
@@ -277,7 +294,7 @@ void orc_epilogue_q8c(int M, const int32_t *acc, int ldacc, const float *a_scale
     for (int n = n0 * 16; n < n1 * 16; n++) {
       float f = (float)acc[(size_t)m * ldacc + n];
       float sc = b_scale[n] * a_scale[m];
-      C[(size_t)m * ldc + n] = f * sc;
+      C[(size_t)m * ldc + n] = orc_fault == 1 ? f * a_scale[m] * b_scale[n] : f * sc;
     }
 }
 
@@ -286,6 +303,19 @@ void orc_epilogue_q8c(int M, const int32_t *acc, int ldacc, const float *a_scale
 void orc_gemm_q8c(int M, int N, int K, const int8_t *Ap, const float *a_scale,
                   const int8_t *B, const float *b_scale, float *C, int ldc, int n0, int n1) {
   if (M <= 0 || n1 <= n0) return;
+  if (orc_fault == 2) {
+    for (int m = 0; m < M; m++)
+      for (int n = n0 * 16; n < n1 * 16; n++) {
+        float c = 0.0f;
+        for (int kb = 0; kb < K / 64; kb++) {
+          int32_t t = 0;
+          for (int k = 64 * kb; k < 64 * kb + 64; k++) t += (int32_t)apk(Ap, K, m, k) * (int32_t)B[b8_off(K, k, n)];
+          c += (float)t;
+        }
+        C[(size_t)m * ldc + n] = c * (a_scale[m] * b_scale[n]);
+      }
+    return;
+  }
   int32_t *acc = (int32_t *)malloc((size_t)M * N * sizeof(int32_t));
   orc_acc_q8c(M, K, Ap, B, acc, N, n0, n1);
   orc_epilogue_q8c(M, acc, N, a_scale, b_scale, C, ldc, n0, n1);
@@ -316,9 +346,17 @@ void orc_epilogue_q4g(int M, int N, int NG, const int32_t *acc, int ldacc, const
   for (int m = 0; m < M; m++)
     for (int n = n0 * 16; n < n1 * 16; n++) {
       float c = 0.0f;
-      for (int g = 0; g < NG; g++)
-        c = fmaf((float)acc[((size_t)g * M + m) * ldacc + n],
-                 orc_f16_to_f32(b_scale[(size_t)g * N + n]), c);
+      for (int i = 0; i < NG; i++) {
+        const int g = orc_fault == 5 ? NG - 1 - i : i;
+        const float a = (float)acc[((size_t)g * M + m) * ldacc + n];
+        const float sc = orc_f16_to_f32(b_scale[(size_t)g * N + n]);
+        if (orc_fault == 4) {
+          const float p = a * sc;
+          c = p + c;
+        } else {
+          c = fmaf(a, sc, c);
+        }
+      }
       C[(size_t)m * ldc + n] = c;
     }
   for (int m = 0; m < M; m++)
@@ -622,6 +660,10 @@ static void orc_attn_head(float *oh, const float *qh, const int8_t *kc, const fl
       lanes[j] = lanes[j] + e;
     }
   float sum = gcc_reduce_add16(lanes);
+  if (orc_fault == 10) {
+    sum = 0.0f;
+    for (int i = 0; i < (n & ~15); i++) sum += sc[i];
+  }
   for (; u < n; u++) {
     const float x = sc[u] - mx;
     sc[u] = expf(x);
@@ -678,6 +720,7 @@ static void orc_attn_head(float *oh, const float *qh, const int8_t *kc, const fl
     const int glo = run_lo[r] & ~3, ghi = (run_hi[r] + 3) & ~3;
     for (int s = glo; s < ghi; s++) {
       if (!iw[s]) continue;
+      if (orc_fault == 11 && r == 1 && s >= (run_lo[0] & ~3) && s < ((run_hi[0] + 3) & ~3)) continue;
       const int8_t *vp = vc + ((size_t)(s >> 2) * kvd + kv_off) * 4 + (s & 3);
       for (int i = 0; i < head_dim; i++) acc[i] += (uint32_t)(iw[s] * (int32_t)vp[(size_t)i * 4]);
     }

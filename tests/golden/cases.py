@@ -241,3 +241,59 @@ def attn_inputs(name: str, n_heads: int, kv_heads: int, head_dim: int, cap: int,
     if n_heads > 1:
         q[head_dim:2 * head_dim] = 0.0
     return q, kv
+
+
+# BASELINE-shaped cases (seeded splitmix64 inputs through the oracle's
+# generators): prep_rows (hsz 0) of fp32 rows, then the GEMM.  The reference's
+# bytes for them are recorded by make_golden.py; the negative controls
+# (tests/test_negative_controls.py) show that plausible wrong epilogues and
+# nibble conventions change them.
+#   name: (kind, M, N, K, group, activation)
+BASELINE_CASES = {
+    "cfg1_q8c_m1": ("q8c", 1, 8192, 2048, 0, "normal"),
+    "cfg2_up_q4g_m8": ("q4g", 8, 8192, 2048, 64, "normal"),
+    "cfg2_down_q4g_m8": ("q4g", 8, 2048, 8192, 64, "normal"),
+    # accumulators past 2^24 whose per-64-k partial sums are not round: the
+    # case that tells a single int32 -> float conversion from float partials
+    "bigacc_q8c_m16": ("q8c", 16, 256, 8192, 0, "bigacc"),
+    # int4 group sums near 2^16 (|a| ~ 120, |w| in 5..8, signs matched), so
+    # (float)acc_g * s needs more than 24 bits: the case that tells the fused
+    # per-group fma from a multiply and an add
+    "bigacc_q4g_m16": ("q4g", 16, 256, 2048, 64, "bigacc"),
+    # cfg5's heavy tail (Student-t nu=3, 0.1% of channels x20), 64 rows
+    "cfg5_down_q8c_m64": ("q8c", 64, 256, 8192, 0, "heavy"),
+}
+
+
+def baseline_inputs(name: str):
+    """(x f32 [M, K], B, bs) of one BASELINE_CASES entry."""
+    kind, M, N, K, group, act = BASELINE_CASES[name]
+    seed = 1000 + sum(ord(c) for c in name)
+    if act == "normal":
+        x = oracle.gen_normal(seed, M * K).reshape(M, K)
+    elif act == "heavy":
+        x = oracle.gen_student_t(seed, M * K, 3).reshape(M, K)
+        hot = np.arange(K) % 1000 == 7             # 0.1% of the channels
+        x[:, hot] *= np.float32(20.0)
+    else:                                          # |x| in [0.8, 1] with random signs
+        mag = oracle.gen_uniform(seed, M * K, 0.8, 1.0)
+        sgn = np.where(oracle.gen_u8(seed + 1, M * K) & 1, 1.0, -1.0).astype(np.float32)
+        x = (mag * sgn).reshape(M, K)
+    if kind == "q8c":
+        if act == "bigacc":                        # weights in +-[100, 127] with A's signs per k
+            w = oracle.gen_i8(seed + 2, N * K, 100, 127).reshape(N, K).astype(np.int16)
+            w = (w * np.where(x[0] < 0, -1, 1)[None, :]).astype(np.int8)
+        else:
+            w = oracle.gen_i8(seed + 2, N * K, -127, 127).reshape(N, K)
+        B = oracle.pack_b_tiles(w)
+        bs = oracle.gen_uniform(seed + 3, N, 1e-3, 1e-2)
+    elif act == "bigacc":                          # int4 in +-[5, 8] with A's signs per k
+        w = oracle.gen_i8(seed + 2, N * K, 5, 8).reshape(N, K).astype(np.int16)
+        w = np.where(x[0] < 0, -1, 1)[None, :] * w
+        w = np.where(w == 8, 7, w).astype(np.int8)     # int4 holds -8..7
+        B = oracle.pack_nibbles(oracle.pack_b_tiles(w))
+        bs = oracle.f32_to_f16(oracle.gen_uniform(seed + 3, (K // group) * N, 5e-3, 5e-2)).reshape(K // group, N)
+    else:
+        B = oracle.gen_u8(seed + 2, N * K // 2)
+        bs = oracle.f32_to_f16(oracle.gen_uniform(seed + 3, (K // group) * N, 5e-3, 5e-2)).reshape(K // group, N)
+    return np.ascontiguousarray(x, np.float32), B, bs

@@ -180,6 +180,18 @@ def main() -> None:
         attn[name] = {"sha256": digest(o), "samples": samples(o)}
     out["attn"] = attn
 
+    base = {}
+    for name, (kind, M, N, K, group, _act) in cases.BASELINE_CASES.items():
+        x, B, bs = cases.baseline_inputs(name)
+        qa = np.zeros((M, K), np.int8)
+        qs = np.zeros(M, np.float32)
+        pa = np.zeros(oracle.packed_a_len(M, K), np.int8)
+        rot = np.zeros((M, K), np.float32)
+        R.fgm_prep_rows(P(x), K, P(rot), P(qa), P(qs), P(pa), M, K, 0, 0, M)
+        C = run_gemm(R, kind, M, N, K, group, 0, N // 16, dict(Ap=pa, a_s=qs, B=B, bs=bs))
+        base[name] = {"prep_sha256": digest(qs, pa), "c_sha256": digest(C), "samples": samples(C)}
+    out["baseline"] = base
+
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_outputs.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)

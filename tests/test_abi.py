@@ -60,6 +60,22 @@ def test_bad_shapes_are_refused_with_einval(args):
     assert L.fgm_hip_last_error()
 
 
+def test_operand_ranges_past_2g_are_refused():
+    """The kernels' buffer descriptors carry 32-bit byte ranges and mask lanes
+    with the offset 2^31: packed A or an int4 scale table of 2^31 bytes or
+    more is refused on the host (B itself is cut into launches along N)."""
+    L = F.lib()
+    # packed A: 16 * ceil(m / 16) * k >= 2^31
+    rc = L.fgm_hip_gemm_q8c_dev(4096, 256, 524288, None, None, None, None, None, 256, 0, 16, None)
+    assert rc == 1 and b"packed A" in L.fgm_hip_last_error()
+    # int4 scales: (k / group) * n * 2 >= 2^31
+    rc = L.fgm_hip_gemm_q4g_dev(8, 1 << 24, 8192, None, None, None, None, 64, None, 1 << 24, 0, 16, None)
+    assert rc == 1 and b"scale table" in L.fgm_hip_last_error()
+    # just below the limits the shape checks pass (ENODEV without a GPU)
+    rc = L.fgm_hip_gemm_q8c_dev(4096, 256, 524224, None, None, None, None, None, 256, 0, 16, None)
+    assert rc in (0, 3) or b"packed A" not in L.fgm_hip_last_error()
+
+
 @pytest.mark.parametrize("group", [0, 32, 96, 192])
 def test_bad_group_is_refused(group):
     L = F.lib()

@@ -1,0 +1,122 @@
+"""GPU edge cases of the GEMM entry points:
+
+* the reference's recorded bytes for the BASELINE.json-shaped golden cases
+  (prep_rows, then the GEMM), the same cases the negative controls use;
+* an empty contraction (k == 0) through the device API writes zeros to
+  columns [16 n0, 16 n1) of rows < m and nothing else (vnni_gemm.c:232-243),
+  with a fill kernel rather than a memset;
+* dense int8 shapes whose K is 64 times an odd number, so a K group's last
+  pipeline stage holds only zero-padded k-blocks;
+* a weight of more than 2^30 bytes, which the library cuts into launches along
+  N with rebased pointers: columns on both sides of each cut against the
+  oracle.
+
+Bar: bit-exact (int32 accumulators and fp32 outputs).
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import hip_util as H
+from tests.golden import cases
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ref_outputs.json")))
+
+
+def _bits_equal(x, y):
+    return np.array_equal(np.ascontiguousarray(x).view(np.uint32), np.ascontiguousarray(y).view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(cases.BASELINE_CASES))
+def test_baseline_golden_cases(name):
+    """GPU prep_rows + GEMM equal the reference's recorded bytes."""
+    from fastgemma_amd import kernels as K
+    kind, M, N, Kd, group, _ = cases.BASELINE_CASES[name]
+    print(name, flush=True)
+    x, B, bs = cases.baseline_inputs(name)
+    t = H.torch()
+    qs = t.zeros(M, device="cuda")
+    pa = t.zeros(oracle.packed_a_len(M, Kd), dtype=t.int8, device="cuda")
+    K.prep_rows(H.dev(x), Kd, None, None, qs, pa, M, Kd, 0, 0, M)
+    C = t.zeros((M, N), device="cuda")
+    if kind == "q8c":
+        K.gemm_q8c(M, N, Kd, pa, qs, H.dev(B), H.dev(bs), C, N, 0, N // 16)
+    else:
+        K.gemm_q4g(M, N, Kd, pa, qs, H.dev(B), H.dev(bs), group, C, N, 0, N // 16)
+    g = GOLD["baseline"][name]
+    assert H.sha(H.host(qs), H.host(pa)) == g["prep_sha256"]
+    assert H.sha(H.host(C)) == g["c_sha256"]
+
+
+@pytest.mark.parametrize("kind", ["q8c", "q4g"])
+@pytest.mark.parametrize("M", [8, 256])
+def test_empty_contraction_writes_zeros_in_range_only(kind, M):
+    from fastgemma_amd import kernels as K
+    t = H.torch()
+    N, ldc, n0, n1 = 256, 272, 4, 12
+    C = t.full((M + 2, ldc), 7.0, device="cuda")
+    one = t.ones(1, device="cuda")
+    dummy = t.zeros(64, dtype=t.int8, device="cuda")
+    if kind == "q8c":
+        K.gemm_q8c(M, N, 0, dummy, one, dummy, one, C, ldc, n0, n1)
+    else:
+        K.gemm_q4g(M, N, 0, dummy, one, dummy.view(t.uint8), dummy.view(t.int16), 64, C, ldc, n0, n1)
+    got = H.host(C)
+    want = np.full((M + 2, ldc), 7.0, np.float32)
+    want[:M, 16 * n0:16 * n1] = 0.0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(2048, 2048, 4160), (256, 2048, 576), (256, 2048, 1088), (256, 512, 8256)])
+def test_dense_odd_k_blocks(M, N, Kd):
+    """K = 64 * odd: the K-group variants end on stages of zero-padded
+    k-blocks (ADVICE: K = 4160 takes the kmin >= 4096 path)."""
+    from fastgemma_amd import kernels as K
+    print("q8c", M, N, Kd, K.gemm_path(8, M, Kd), flush=True)
+    A = oracle.gen_i8(17 + Kd, M * Kd, -127, 127).reshape(M, Kd)
+    Ap = oracle.pack_a(M, Kd, A)
+    a_s = oracle.gen_uniform(18 + Kd, M, 1e-3, 1e-2)
+    B = oracle.gen_i8(19 + Kd, N * Kd, -127, 127)
+    bs = oracle.gen_uniform(20 + Kd, N, 1e-3, 1e-2)
+    acc = H.gpu_acc("q8c", M, N, Kd, Ap, B)
+    want = H.exact_acc(A, H.decode_b8(B, N, Kd))
+    assert np.array_equal(acc, want)
+    C = H.gpu_gemm("q8c", M, N, Kd, Ap, a_s, B, bs)
+    R = want.astype(np.float32) * (bs[None, :] * a_s[:, None])
+    assert _bits_equal(C, R.astype(np.float32))
+
+
+@pytest.mark.parametrize("M", [8, 128])
+def test_weight_past_1gib_is_cut_along_n(M):
+    """int8 N=73728 K=16384 (1.21 GB of weights): launches of at most 2^30
+    bytes of B, i.e. 4096 n-blocks each; n-blocks at the start, on both sides
+    of the cut and at the end equal the oracle on the same bytes."""
+    from fastgemma_amd import kernels as K
+    t = H.torch()
+    N, Kd = 73728, 16384
+    print("q8c chunked", M, N, Kd, K.gemm_path(8, M, Kd), flush=True)
+    g = t.Generator(device="cuda")
+    g.manual_seed(1234 + M)
+    B = t.randint(-127, 128, (N * Kd,), dtype=t.int8, device="cuda", generator=g)
+    bs = t.rand(N, device="cuda", generator=g) * 0.009 + 0.001
+    A = oracle.gen_i8(55 + M, M * Kd, -127, 127).reshape(M, Kd)
+    Ap = oracle.pack_a(M, Kd, A)
+    a_s = oracle.gen_uniform(56 + M, M, 1e-3, 1e-2)
+    C = t.full((M, N), 3.0, device="cuda")
+    K.gemm_q8c(M, N, Kd, H.dev(Ap), H.dev(a_s), B, bs, C, N, 0, N // 16)
+    got = H.host(C)
+    for nb0, nb1 in ((0, 4), (4092, 4100), (N // 16 - 4, N // 16)):
+        sub = H.host(B[nb0 * Kd * 16:nb1 * Kd * 16])
+        sbs = H.host(bs[16 * nb0:16 * nb1])
+        n = 16 * (nb1 - nb0)
+        R = np.zeros((M, n), np.float32)
+        oracle.gemm_q8c(M, n, Kd, Ap, a_s, sub, sbs, R, n, 0, n // 16)
+        assert _bits_equal(got[:, 16 * nb0:16 * nb1], R), (nb0, nb1)
+    del B

@@ -107,3 +107,38 @@ def test_bad_files(tmp_path):
         Model(str(p))
     with pytest.raises(FgmHipError, match="cannot open"):
         Model(str(tmp_path / "missing.fgm"))
+
+
+def _linear_file(path, n, k, wbytes, sbytes, dtype="q4g", group=64):
+    out = [("w", np.zeros(wbytes, np.uint8), dtype, (n, k), {"group": group} if dtype == "q4g" else {}),
+           ("w.scale", np.zeros(sbytes, np.uint8), "f16" if dtype == "q4g" else "f32",
+            ((k // max(group, 1)), n) if dtype == "q4g" else (n,), None)]
+    fgm_file.write_fgm(str(path), {}, out)
+
+
+@pytest.mark.parametrize("n,k,wb,sb,dtype,group,msg", [
+    (256, 512, 256 * 512 // 2 - 1, (512 // 64) * 256 * 2, "q4g", 64, "its shape needs"),   # short blob
+    (256, 512, 256 * 512 // 2, (512 // 64) * 256 * 2 - 2, "q4g", 64, "needs"),             # short scales
+    (256, 512, 256 * 512, 256 * 4 - 4, "q8c", 0, "needs"),                                  # short f32 scales
+    (250, 512, 250 * 512, 250 * 4, "q8c", 0, "n % 16"),                                     # n not tiled
+    (256, 500, 256 * 500, 256 * 4, "q8c", 0, "k % 64"),                                     # k not tiled
+    (256, 512, 256 * 512 // 2, 4096, "q4g", 96, "group"),                                   # bad group
+    (0, 512, 64, 64, "q8c", 0, "shape"),                                                    # empty
+])
+def test_linear_refuses_malformed_tensors(tmp_path, n, k, wb, sb, dtype, group, msg):
+    """Model::linear on a tensor whose bytes or shape the GEMM cannot read
+    safely: refused with EINVAL on the host instead of a device read past the
+    tensor's end."""
+    p = tmp_path / "lin.fgm"
+    _linear_file(p, n, k, wb, sb, dtype, group)
+    with Model(str(p)) as m:
+        with pytest.raises(FgmHipError, match=msg):
+            m.linear("w")
+
+
+def test_linear_accepts_exact_sizes(tmp_path):
+    p = tmp_path / "ok.fgm"
+    _linear_file(p, 256, 512, 256 * 512 // 2, (512 // 64) * 256 * 2)
+    with Model(str(p)) as m:
+        w = m.linear("w")
+        assert (w.bits, w.n, w.k, w.group) == (4, 256, 512, 64)
