@@ -134,10 +134,14 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_hip_linear_scratch_bytes.argtypes = [i, i]
     L.fgm_hip_linear_scratch_bytes.restype = _C.c_size_t
     L.fgm_hip_linear_run_dev.argtypes = [p, p, i, i, p, p, _C.c_size_t, p]
+    L.fgm_hip_linear_run_noalloc_dev.argtypes = [p, p, i, i, p, p]
+    L.fgm_hip_linear_noalloc_max_bytes.argtypes = []
+    L.fgm_hip_linear_noalloc_max_bytes.restype = _C.c_size_t
     for name in ("fgm_hip_model_has", "fgm_hip_model_tensor_count", "fgm_hip_model_tensor",
                  "fgm_hip_model_linear", "fgm_hip_weight_sel", "fgm_hip_model_dual",
                  "fgm_hip_model_gather_dev", "fgm_hip_gather_dev", "fgm_hip_pool_gemm_dev",
-                 "fgm_hip_pool_prep_dev", "fgm_hip_linear_run_dev"):
+                 "fgm_hip_pool_prep_dev", "fgm_hip_linear_run_dev",
+                 "fgm_hip_linear_run_noalloc_dev"):
         getattr(L, name).restype = i
     for name in ("fgm_hip_attend_dev", "fgm_hip_attend_heads_dev", "fgm_hip_store_v_t_dev",
                  "fgm_hip_kv_store_dev", "fgm_hip_gemm_batch_dev", "fgm_hip_prep_batch_dev",

@@ -28,6 +28,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -668,6 +669,60 @@ int fgm_hip_linear_run_dev(const fgm_hip_linear* w, const float* a, int m, int l
   if (w->bits == 4) j.bq = (const uint8_t*)w->b, j.s4 = (const uint16_t*)w->b_scale;
   else j.b8 = (const int8_t*)w->b, j.s8 = (const float*)w->b_scale;
   return fgm_hip_pool_gemm_dev(&j, stream);
+}
+
+// ------------------------------------------------- the allocation-free run
+// fgm_hip_linear_run_dev with its scratch (row scales + packed activation) in
+// a file-scope device array instead of a caller buffer, for callers that must
+// not allocate (graph capture, serving loops).  Each GPU holds its own copy
+// of the array for the life of the process; its device address is looked up
+// once per device and kept, since the array's name is only a host-side
+// stand-in in host code.  Every call on a GPU shares that GPU's array, so
+// calls that overlap on one GPU (different streams, concurrent graphs) race.
+// Nothing in the array has to start at zero: the prep writes every row scale
+// and every packed-A byte the GEMM reads, pad rows included.
+constexpr size_t FGM_NOALLOC_SCRATCH_BYTES = (size_t)8 << 20;
+static __device__ __align__(256) char scratch[FGM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int FGM_NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_ptr[FGM_NOALLOC_MAX_DEVICES];
+
+// this device's copy of `scratch` (nullptr and a status on failure)
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "linear (no-alloc): hipGetDevice");
+  if (dev < 0 || dev >= FGM_NOALLOC_MAX_DEVICES)
+    return fail(FGM_HIP_EINVAL, "linear (no-alloc): device %d beyond %d", dev, FGM_NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "linear (no-alloc): scratch address");
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = g_noalloc_ptr[dev];
+  return FGM_HIP_OK;
+}
+}  // namespace
+
+size_t fgm_hip_linear_noalloc_max_bytes(void) { return FGM_NOALLOC_SCRATCH_BYTES; }
+
+int fgm_hip_linear_run_noalloc_dev(const fgm_hip_linear* w, const float* a, int m, int lda, float* out,
+                                   void* stream) {
+  if (!w || !w->b || !w->b_scale) return fail(FGM_HIP_EINVAL, "linear: no device weights (open the model resident)");
+  if (m <= 0) return FGM_HIP_OK;
+  const size_t need = fgm_hip_linear_scratch_bytes(m, w->k);
+  if (need > FGM_NOALLOC_SCRATCH_BYTES)
+    return fail(FGM_HIP_EINVAL, "linear (no-alloc): m=%d k=%d needs %zu scratch bytes, the limit is %zu", m, w->k,
+                need, FGM_NOALLOC_SCRATCH_BYTES);
+  int rc = ensure_device();
+  if (rc) return rc;
+  void* p = nullptr;
+  if ((rc = noalloc_scratch(&p))) return rc;
+  return fgm_hip_linear_run_dev(w, a, m, lda, out, p, FGM_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 void fgm_gather_q8r_hip(float* out, const int8_t* tbl, const float* sc, int row, int k) {

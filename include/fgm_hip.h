@@ -322,6 +322,18 @@ size_t fgm_hip_linear_scratch_bytes(int m, int k);
 int fgm_hip_linear_run_dev(const fgm_hip_linear *w, const float *a, int m, int lda, float *out,
                            void *scratch, size_t scratch_bytes, void *stream);
 
+/* fgm_hip_linear_run_dev without a scratch argument and with no allocation:
+ * the scratch lives in a file-scope device array of
+ * fgm_hip_linear_noalloc_max_bytes() bytes (8 MiB) per GPU, held until the
+ * process ends.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, serving loops).  Shapes
+ * whose fgm_hip_linear_scratch_bytes(m, k) exceeds the limit are refused with
+ * FGM_HIP_EINVAL.  All calls on one GPU share the array: calls that overlap on
+ * one GPU (several streams, concurrent graphs) race. */
+size_t fgm_hip_linear_noalloc_max_bytes(void);
+int fgm_hip_linear_run_noalloc_dev(const fgm_hip_linear *w, const float *a, int m, int lda, float *out,
+                                   void *stream);
+
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);
