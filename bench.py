@@ -357,6 +357,68 @@ def extra_cfg5(gpu):
     return {"workload": "long prefill M=2048 (gate/up int4 g64, down int8)", "per_shape": res}
 
 
+def extra_ceilings(gpu):
+    """The floors the roofline fractions are read against, measured on this box
+    by fastgemma_amd/csrc/fgm_ceil.hip: the back-to-back launch floor, pure-read
+    floors at the decode sizes (rotating buffers, so each read comes from
+    HBM), a plain copy (the kernel that calibrates FETCH_SIZE / WRITE_SIZE),
+    and the dense int8 MFMA rate with independent chains on every SIMD."""
+    import ctypes as C
+    L = C.CDLL(os.path.join(ROOT, "fastgemma_amd", "libfgm_ceil.so"))
+    L.fgm_ceil_empty.argtypes = [C.c_int, C.c_int, C.c_void_p]
+    L.fgm_ceil_read.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p]
+    L.fgm_ceil_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    L.fgm_ceil_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    t = gpu.t
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(f"fgm_ceil call failed: {rc}")
+
+    res = {}
+    for nwg, thr in ((1, 64), (256, 256), (256, 1024)):
+        dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_empty(nwg, thr, gpu.stream())), 64, 5)
+        res[f"empty_launch_{nwg}x{thr}_us"] = dt * 1e6
+    chunk = 256 * 16 * 8
+    sink = t.zeros(600 * 1000 * 1000 // 4096, dtype=t.int32, device=gpu.dev)
+    reads = {}
+    for mb, copies in ((18, 48), (134, 6), (537, 2)):
+        nbytes = (mb * 1000 * 1000) // chunk * chunk
+        bufs = [t.empty(nbytes, dtype=t.uint8, device=gpu.dev) for _ in range(copies)]
+        best = None
+        for u in (1, 2, 4, 8):
+            dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_read(bufs[i % copies].data_ptr(), nbytes, u,
+                                                              sink.data_ptr(), gpu.stream())),
+                            max(copies, 8), 3)
+            if best is None or dt < best[0]:
+                best = (dt, u)
+        reads[f"{mb}MB"] = {"bytes": nbytes, "us": best[0] * 1e6, "GB_s": nbytes / best[0] / 1e9,
+                            "frac_hbm": nbytes / best[0] / HBM_PEAK,
+                            "bytes_per_workgroup": 4096 * best[1]}
+        del bufs
+        t.cuda.empty_cache()
+    res["read_one_launch"] = reads
+    nbytes = 512 << 20
+    src = t.empty(nbytes, dtype=t.uint8, device=gpu.dev)
+    dst = t.empty(nbytes, dtype=t.uint8, device=gpu.dev)
+    dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_copy(src.data_ptr(), dst.data_ptr(), nbytes, 4096,
+                                                      gpu.stream())), 4, 3)
+    res["copy_512MiB"] = {"bytes_read": nbytes, "bytes_written": nbytes, "us": dt * 1e6,
+                          "GB_s": 2 * nbytes / dt / 1e9}
+    del src, dst
+    t.cuda.empty_cache()
+    iters = 2000
+    for shape, ops1 in ((32, 65536), (16, 32768)):
+        nwg = 1024
+        dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_mfma(shape, nwg, iters, sink.data_ptr(),
+                                                          gpu.stream())), 4, 3)
+        ops = nwg * 4 * iters * 4 * ops1
+        res[f"mfma_i8_{shape}"] = {"TOPS": ops / dt / 1e12, "frac_of_5000": ops / dt / I8_PEAK,
+                                   "us": dt * 1e6}
+    return {"workload": "ceiling probes (fgm_ceil.hip): launch floor, one-launch read floors, "
+                        "copy, int8 MFMA rate", **res}
+
+
 def extra_elem(gpu):
     """The elementwise primitives between the GEMMs (rmsnorm, gelu_mul, rope,
     add, softcap), at the model's decode (M=8) and prefill (M=256, 2048)
@@ -669,7 +731,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
-                    help="run one extra measurement (cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
+                    help="run one extra measurement (ceilings, cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
                          "prep_fused, attn, model) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -680,7 +742,8 @@ def main():
 
     gpu = Gpu()
     gpu.t.manual_seed(1234)
-    extras = {"cfg1": extra_cfg1, "int4_stream": extra_int4_stream, "cfg3": extra_cfg3,
+    extras = {"ceilings": extra_ceilings, "cfg1": extra_cfg1, "int4_stream": extra_int4_stream,
+              "cfg3": extra_cfg3,
               "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem,
               "prep_fused": extra_prep_fused, "attn": extra_attn,
               "model": extra_model}
