@@ -73,16 +73,6 @@ constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thre
 #define FGM_DEC_NWMIN 4           // smallest number of stream waves per workgroup
 #endif
 
-static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
-FGM_DEV GemmProb pick(const GemmBatch& bt) {
-  const int b = blockIdx.x;
-  GemmProb p = bt.p[0];
-  if (bt.count > 1 && b >= bt.p[1].wg0) p = bt.p[1];
-  if (bt.count > 2 && b >= bt.p[2].wg0) p = bt.p[2];
-  if (bt.count > 3 && b >= bt.p[3].wg0) p = bt.p[3];
-  return p;
-}
-
 // Two 16-byte LDS reads by byte address, and waits for all but the last six
 // LDS operations (or for all of them) that also order the use of the given
 // registers after the wait.  LDS operations complete in issue order.
@@ -163,7 +153,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   using G = Geo<BITS, MB, HALF>;
   constexpr int TPU = G::TPU, OUT = G::OUT, NA = G::NA, X = G::X, D = G::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const GemmProb a = pick(bt);
+  const GemmProb a = pick_problem(bt);
   const int tid = threadIdx.x, NT = blockDim.x;
   const int w = wave_id(), l = tid & 63, g = l >> 4, j = l & 15;
   const int M = a.M, N = a.N, KB = a.K >> 6;
@@ -583,6 +573,7 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
     if (need > lds) lds = need;
   }
   if (nwg == 0) return hipSuccess;
+  close_batch(bt);
   // the kernel derives a problem's stream waves as KS * NBW; pad the others
   // up to the launch's NWS with idle n-blocks is not needed: every problem
   // uses NBW = NWS / KS unless its n-blocks run out

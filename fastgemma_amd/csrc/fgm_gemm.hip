@@ -41,16 +41,6 @@ namespace {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
-FGM_DEV GemmProb pick(const GemmBatch& bt) {
-  const int b = blockIdx.x;
-  GemmProb p = bt.p[0];
-  if (bt.count > 1 && b >= bt.p[1].wg0) p = bt.p[1];
-  if (bt.count > 2 && b >= bt.p[2].wg0) p = bt.p[2];
-  if (bt.count > 3 && b >= bt.p[3].wg0) p = bt.p[3];
-  return p;
-}
-
 FGM_DEV v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
@@ -93,7 +83,7 @@ template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, 
 __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const GemmProb a = pick(bt);
+  const GemmProb a = pick_problem(bt);
   const int tid = threadIdx.x, wv = wave_id(), l = tid & 63, h = l >> 5, l32 = l & 31;
   // K group kg, wave w within it
   const int kg = wv / C::NWG, w = wv - kg * C::NWG;
@@ -443,6 +433,7 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
     nwg += ((p.M + C::BM - 1) / C::BM) * ((p.nblocks + C::NBL - 1) / C::NBL);
   }
   if (nwg == 0) return hipSuccess;
+  close_batch(b);
   hipLaunchKernelGGL(k, dim3(nwg), dim3(C::T), C::LDS, st, b);
   return hipGetLastError();
 }

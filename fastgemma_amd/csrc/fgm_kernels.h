@@ -6,9 +6,29 @@
 #include <stddef.h>
 #include <stdint.h>
 
-// Independent problems served by one launch.  The kernels' pick() selects a
-// problem with four unrolled comparisons; it asserts this value.
+// Independent problems served by one launch.
 constexpr int FGM_MAX_BATCH = 4;
+
+// The problem workgroup blockIdx.x belongs to: problem i owns workgroups
+// [p[i].wg0, p[i + 1].wg0), and the launcher sets wg0 = INT_MAX in the slots
+// past the batch.  Every wg0 is read in one round of scalar loads and the
+// index is formed without branches, then the chosen problem is read by that
+// index: two dependent argument fetches at kernel start, not one per
+// problem (each is a memory round trip while the argument lines are cold).
+template <class Batch>
+__device__ __forceinline__ auto pick_problem(const Batch& bt) {
+  const int b = blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < FGM_MAX_BATCH; k++) i += b >= bt.p[k].wg0 ? 1 : 0;
+  return bt.p[__builtin_amdgcn_readfirstlane(i)];
+}
+
+// wg0 of the slots past the batch (see pick_problem)
+template <class Batch>
+inline void close_batch(Batch& bt) {
+  for (int k = bt.count; k < FGM_MAX_BATCH; k++) bt.p[k].wg0 = 0x7FFFFFFF;
+}
 
 struct GemmProb {
   const int8_t* A;        // packed A [ceil(M/16)][K/64][16][64]

@@ -100,18 +100,6 @@ __device__ __forceinline__ size_t pa_off(int row, int col, int KB) {
   return (((size_t)(row >> 4) * KB + (col >> 6)) * 16 + (row & 15)) * 64 + (col & 63);
 }
 
-// The problem a workgroup belongs to, chosen with uniform selects so the
-// kernel-argument array is never indexed dynamically.
-static_assert(FGM_MAX_BATCH == 4, "pick() compares four problems");
-__device__ __forceinline__ PrepProb pick(const PrepBatch& bt) {
-  const int b = blockIdx.x;
-  PrepProb p = bt.p[0];
-  if (bt.count > 1 && b >= bt.p[1].wg0) p = bt.p[1];
-  if (bt.count > 2 && b >= bt.p[2].wg0) p = bt.p[2];
-  if (bt.count > 3 && b >= bt.p[3].wg0) p = bt.p[3];
-  return p;
-}
-
 // The computing part of prep_rows_kernel for a row whose float4s fit NV per
 // thread (4 T NV >= k).  Every per-float4 loop is fully unrolled with no
 // bound checks: float4s past the row read 0 through the buffer range check,
@@ -391,7 +379,7 @@ template <int PRE>
 __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
   __shared__ float red[PREP_MAX_THREADS / 64];
-  const PrepProb a = pick(bt);
+  const PrepProb a = pick_problem(bt);
   const int row = a.r0 + (blockIdx.x - a.wg0);
   const int k = a.k, KB = k >> 6;
   const int T = blockDim.x, tid = threadIdx.x;
@@ -491,6 +479,7 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
     }
   }
   if (nwg == 0) return hipSuccess;
+  close_batch(b);
   // One float4 per thread up to 512 threads (gelu_mul, heavier per element:
   // 1024), more float4s per thread beyond, at most VMAX: a row's work is
   // latency-bound at the decode sizes, so more waves per row pay until the
