@@ -296,15 +296,69 @@ int cached_upload(const void* host, size_t bytes, void** dev) {
   return FGM_HIP_OK;
 }
 
-// Per-thread stream and grow-only device staging buffers for the drop-ins.
-// They live until the process ends (no destructor: freeing device memory
-// while the HIP runtime is being torn down at exit is not safe).
+// Per-thread stream and grow-only staging buffers for the drop-ins: device
+// buffers, and pinned host buffers through which the caller's (pageable)
+// arrays move, so that each call is one host-to-device DMA, the launches and
+// one device-to-host DMA, with a memcpy on either side.  They live until the
+// process ends (no destructor: freeing device memory while the HIP runtime is
+// being torn down at exit is not safe).
 struct Staging {
   hipStream_t st = nullptr;
   void* buf[8] = {};
   size_t cap[8] = {};
+  void* pin[2] = {};
+  size_t pcap[2] = {};
 };
-thread_local Staging g_stage;
+// A thread takes a context on its first drop-in call and hands it back to a
+// free list when it exits, where the next new thread finds it: callers that
+// start threads per call (or per batch) reuse the buffers and stream instead
+// of leaking a set per thread.  The list is never destroyed.
+struct StagingPool {
+  std::mutex mu;
+  std::vector<Staging*> free;
+};
+StagingPool& stage_pool() {
+  static StagingPool* p = new StagingPool;
+  return *p;
+}
+struct StageHolder {
+  Staging* s = nullptr;
+  Staging& get() {
+    if (!s) {
+      StagingPool& pl = stage_pool();
+      std::lock_guard<std::mutex> lk(pl.mu);
+      if (!pl.free.empty()) {
+        s = pl.free.back();
+        pl.free.pop_back();
+      } else {
+        s = new Staging;
+      }
+    }
+    return *s;
+  }
+  ~StageHolder() {
+    if (!s) return;
+    StagingPool& pl = stage_pool();
+    std::lock_guard<std::mutex> lk(pl.mu);
+    pl.free.push_back(s);
+  }
+};
+thread_local StageHolder g_stage_holder;
+#define g_stage (g_stage_holder.get())
+
+int pinned(int slot, size_t bytes, void** out) {
+  if (g_stage.pcap[slot] < bytes) {
+    if (g_stage.pin[slot]) HIPCHK(hipHostFree(g_stage.pin[slot]));
+    g_stage.pin[slot] = nullptr;
+    g_stage.pcap[slot] = 0;
+    HIPCHK(hipHostMalloc(&g_stage.pin[slot], bytes ? bytes : 1, hipHostMallocDefault));
+    g_stage.pcap[slot] = bytes;
+  }
+  *out = g_stage.pin[slot];
+  return FGM_HIP_OK;
+}
+
+inline size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int staging(int slot, size_t bytes, void** out) {
   if (!g_stage.st) HIPCHK(hipStreamCreate(&g_stage.st));
@@ -335,20 +389,27 @@ int dropin_gemm(int bits, int m, int n, int k, const int8_t* a, const float* a_s
   if ((rc = cached_upload(b_scale, sbytes, &ds))) return rc;
   const size_t abytes = packed_a_len(m, k);
   const int wcols = 16 * (n1 - n0);
-  if ((rc = staging(0, abytes, &da)) || (rc = staging(1, (size_t)m * 4, &das)) ||
-      (rc = staging(2, (size_t)m * wcols * 4, &dc)))
+  const size_t cbytes = (size_t)m * wcols * 4;
+  // in: [packed A | a_scale]; out: the written columns of C, contiguous
+  const size_t inb = up256(abytes) + (size_t)m * 4;
+  void *pin_in, *pin_out;
+  if ((rc = staging(0, inb, &da)) || (rc = staging(2, cbytes, &dc)) || (rc = pinned(0, inb, &pin_in)) ||
+      (rc = pinned(1, cbytes, &pin_out)))
     return rc;
+  das = (char*)da + up256(abytes);
   hipStream_t st = g_stage.st;
-  HIPCHK(hipMemcpyAsync(da, a, abytes, hipMemcpyHostToDevice, st));
-  HIPCHK(hipMemcpyAsync(das, a_scale, (size_t)m * 4, hipMemcpyHostToDevice, st));
+  memcpy(pin_in, a, abytes);
+  memcpy((char*)pin_in + up256(abytes), a_scale, (size_t)m * 4);
+  HIPCHK(hipMemcpyAsync(da, pin_in, inb, hipMemcpyHostToDevice, st));
   // the kernel indexes C by absolute column; point it 16*n0 columns early
   float* cbase = (float*)dc - 16 * n0;
   if ((rc = run_gemm(bits, m, n, k, (const int8_t*)da, (const float*)das, db, ds, group, cbase,
                      wcols, n0, n1, nullptr, 0, st)))
     return rc;
-  HIPCHK(hipMemcpy2DAsync(c + 16 * n0, (size_t)ldc * 4, dc, (size_t)wcols * 4, (size_t)wcols * 4,
-                          m, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(pin_out, dc, cbytes, hipMemcpyDeviceToHost, st));
   HIPCHK(hipStreamSynchronize(st));
+  for (int r = 0; r < m; r++)
+    memcpy(c + (size_t)r * ldc + 16 * n0, (const float*)pin_out + (size_t)r * wcols, (size_t)wcols * 4);
   return FGM_HIP_OK;
 }
 
@@ -597,30 +658,40 @@ static int dropin_prep(const float* src, int lda, float* rot, int8_t* qa, float*
   const int n = r1 - r0;
   const int blk_end = ((r1 + 15) / 16) * 16;
   const int qa_end = blk_end < m ? blk_end : m;  // rows of qa the pack reads
-  void *dsrc, *drot, *dqa, *dqs, *dpa;
-  if ((rc = staging(0, (size_t)n * k * 4, &dsrc)) || (rc = staging(1, (size_t)n * k * 4, &drot)) ||
-      (rc = staging(2, (size_t)(qa_end - r0) * k, &dqa)) || (rc = staging(3, (size_t)n * 4, &dqs)) ||
-      (rc = staging(4, (size_t)(blk_end - r0) * k, &dpa)))
+  // One staging layout on both sides, rows [r0, ...) only:
+  //   in : src rows [n][k] f32, then the qa rows [r1, qa_end) the pack reads
+  //   out: rot [n][k] f32 | qa [qa_end - r0][k] | qs [n] f32 | pa [blk_end - r0][k]
+  const size_t o_src = 0, o_qin = up256((size_t)n * k * 4);
+  const size_t inb = o_qin + (size_t)(qa_end - r1) * k;
+  const size_t o_rot = 0, o_qa = up256((size_t)n * k * 4), o_qs = o_qa + up256((size_t)(qa_end - r0) * k),
+               o_pa = o_qs + up256((size_t)n * 4), outb = o_pa + (size_t)(blk_end - r0) * k;
+  void *din, *dout, *pin_in, *pin_out;
+  if ((rc = staging(0, inb, &din)) || (rc = staging(1, outb, &dout)) || (rc = pinned(0, inb, &pin_in)) ||
+      (rc = pinned(1, outb, &pin_out)))
     return rc;
   hipStream_t st = g_stage.st;
-  // device buffers hold rows [r0, ...) only; offset the bases so row indices stay absolute
-  HIPCHK(hipMemcpy2DAsync(dsrc, (size_t)k * 4, src + (size_t)r0 * lda, (size_t)lda * 4,
-                          (size_t)k * 4, n, hipMemcpyHostToDevice, st));
-  if (qa_end > r1)
-    HIPCHK(hipMemcpyAsync((int8_t*)dqa + (size_t)n * k, qa + (size_t)r1 * k,
-                          (size_t)(qa_end - r1) * k, hipMemcpyHostToDevice, st));
-  const float* bsrc = (const float*)dsrc - (size_t)r0 * k;
-  float* brot = (float*)drot - (size_t)r0 * k;
-  int8_t* bqa = (int8_t*)dqa - (size_t)r0 * k;
-  float* bqs = (float*)dqs - r0;
-  int8_t* bpa = (int8_t*)dpa - (size_t)r0 * k;  // r0 % 16 == 0: tile blocks start at r0
+  for (int r = 0; r < n; r++)
+    memcpy((float*)((char*)pin_in + o_src) + (size_t)r * k, src + (size_t)(r0 + r) * lda, (size_t)k * 4);
+  if (qa_end > r1) memcpy((char*)pin_in + o_qin, qa + (size_t)r1 * k, (size_t)(qa_end - r1) * k);
+  HIPCHK(hipMemcpyAsync(din, pin_in, inb, hipMemcpyHostToDevice, st));
+  char* dq = (char*)dout + o_qa;
+  if (qa_end > r1)  // the rows the pack copies from qa, in place in the output image
+    HIPCHK(hipMemcpyAsync(dq + (size_t)n * k, (char*)din + o_qin, (size_t)(qa_end - r1) * k,
+                          hipMemcpyDeviceToDevice, st));
+  // device images hold rows [r0, ...) only; offset the bases so row indices stay absolute
+  const float* bsrc = (const float*)((char*)din + o_src) - (size_t)r0 * k;
+  float* brot = (float*)((char*)dout + o_rot) - (size_t)r0 * k;
+  int8_t* bqa = (int8_t*)dq - (size_t)r0 * k;
+  float* bqs = (float*)((char*)dout + o_qs) - r0;
+  int8_t* bpa = (int8_t*)((char*)dout + o_pa) - (size_t)r0 * k;  // r0 % 16 == 0: tile blocks start at r0
   if ((rc = fgm_hip_prep_rows_dev(bsrc, k, brot, bqa, bqs, bpa, m, k, hsz, r0, r1, st))) return rc;
-  HIPCHK(hipMemcpyAsync(rot + (size_t)r0 * k, drot, (size_t)n * k * 4, hipMemcpyDeviceToHost, st));
-  HIPCHK(hipMemcpyAsync(qa + (size_t)r0 * k, dqa, (size_t)n * k, hipMemcpyDeviceToHost, st));
-  HIPCHK(hipMemcpyAsync(qs + r0, dqs, (size_t)n * 4, hipMemcpyDeviceToHost, st));
-  HIPCHK(hipMemcpyAsync(pa + (size_t)r0 * k, dpa, (size_t)(blk_end - r0) * k, hipMemcpyDeviceToHost,
-                        st));
+  HIPCHK(hipMemcpyAsync(pin_out, dout, outb, hipMemcpyDeviceToHost, st));
   HIPCHK(hipStreamSynchronize(st));
+  const char* po = (const char*)pin_out;
+  memcpy(rot + (size_t)r0 * k, po + o_rot, (size_t)n * k * 4);
+  memcpy(qa + (size_t)r0 * k, po + o_qa, (size_t)n * k);
+  memcpy(qs + r0, po + o_qs, (size_t)n * 4);
+  memcpy(pa + (size_t)r0 * k, po + o_pa, (size_t)(blk_end - r0) * k);
   return FGM_HIP_OK;
 }
 

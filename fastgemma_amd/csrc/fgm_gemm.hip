@@ -382,15 +382,19 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
     if (kg > 0) return;
   }
 
-  // ---- epilogue: one buffer store per output; rows past M fall outside the
-  // tile's buffer range, columns past n1 are masked
+  // ---- epilogue: one buffer store per output.  The buffer starts at the
+  // tile's first row and column (callers may pass C shifted so that column
+  // 16 n0 is its first stored one) and ends after the tile's last stored
+  // element: rows past M fall outside it, columns past n1 are masked.
   if (BITS == 4 && RAW) return;
   const int mrow0 = mtile * C::BM;
   const int mrows = M - mrow0 < C::BM ? M - mrow0 : C::BM;
   const int ld = RAW ? a.ldacc : a.ldc;
-  const void* obase = RAW ? (const void*)(a.acc_out + (size_t)mrow0 * a.ldacc)
-                          : (const void*)(a.C + (size_t)mrow0 * a.ldc);
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(obase, (uint32_t)mrows * (uint32_t)ld * 4u);
+  const int ncols = nbend * 16 - nb0 * 16 < C::BN ? nbend * 16 - nb0 * 16 : C::BN;
+  const size_t o0 = (size_t)mrow0 * ld + (size_t)nb0 * 16;
+  const void* obase = RAW ? (const void*)(a.acc_out + o0) : (const void*)(a.C + o0);
+  const __amdgpu_buffer_rsrc_t ro =
+      make_rsrc(obase, ((uint32_t)(mrows - 1) * (uint32_t)ld + (uint32_t)ncols) * 4u);
 #pragma unroll
   for (int y = 0; y < WNT; y++) {
     const int coll = wn * WNT * 32 + y * 32 + l32, n = nb0 * 16 + coll;
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
           if (BITS == 8 && RAW) v = (uint32_t)acc[x][y][r];
           else if (BITS == 8) v = __float_as_uint((float)acc[x][y][r] * (bsn * ase));
           else v = __float_as_uint(cf[x][y][r] * ase);
-          __builtin_amdgcn_raw_buffer_store_b32(v, ro, (int)(((uint32_t)(rowq + e) * (uint32_t)ld + (uint32_t)n) * 4u), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(v, ro, (int)(((uint32_t)(rowq + e) * (uint32_t)ld + (uint32_t)coll) * 4u), 0, 0);
         }
       }
   }
