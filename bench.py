@@ -419,6 +419,22 @@ def extra_ceilings(gpu):
                         "copy, int8 MFMA rate", **res}
 
 
+def extra_vendor(gpu):
+    """The vendor int8 GEMM (torch._int_mm, served by hipBLASLt / rocBLAS on
+    ROCm) on the prefill shapes, int32 output, no scales: a reference point
+    for the dense kernel (which also runs the fp32 epilogue), not part of the
+    path."""
+    t = gpu.t
+    res = {}
+    for name, M, N, K in (("q", 256, 2048, 2048), ("k", 256, 512, 2048), ("gate", 256, 8192, 2048),
+                          ("down", 256, 2048, 8192), ("cfg5_down", 2048, 2048, 8192)):
+        A = t.randint(-127, 128, (M, K), dtype=t.int8, device=gpu.dev)
+        Bs = [t.randint(-127, 128, (N, K), dtype=t.int8, device=gpu.dev) for _ in range(8)]
+        dt = kernel_avg(gpu, lambda i: t._int_mm(A, Bs[i % 8].t()), 16, 3)
+        res[name] = {"us": dt * 1e6, "TOPS": 2.0 * M * N * K / dt / 1e12}
+    return {"workload": "torch._int_mm (vendor int8 GEMM), int32 out, graphs of 16", "per_shape": res}
+
+
 def extra_elem(gpu):
     """The elementwise primitives between the GEMMs (rmsnorm, gelu_mul, rope,
     add, softcap), at the model's decode (M=8) and prefill (M=256, 2048)
@@ -688,7 +704,31 @@ def cpu_baseline(host, budget_s=10.0):
         t0 = time.perf_counter()
         one_step()
         times.append(time.perf_counter() - t0)
+
+    # the prefill row beside it: BASELINE configs[2]'s q projection (M=256,
+    # N=2048, K=2048, int8 per-channel) through the reference's
+    # fgm_gemm_q8c_vnni with the same N-split, for about a quarter of the budget
+    fq8 = C.cast(R.fgm_gemm_q8c_vnni if R is not None else L.orc_gemm_q8c, C.c_void_p).value
+    Mp, Np, Kp = 256, 2048, 2048
+    ap = oracle.gen_i8(21, Mp * Kp, -127, 127)
+    pa8 = oracle.pack_a(Mp, Kp, ap.reshape(Mp, Kp))
+    as8 = oracle.gen_uniform(22, Mp, 1e-3, 1e-2)
+    w8 = oracle.gen_i8(23, Np * Kp, -127, 127)
+    s8 = oracle.gen_uniform(24, Np, 1e-3, 1e-2)
+    c8 = np.empty((Mp, Np), np.float32)
+
+    def one_gemm():
+        L.orc_pool_q8c(fq8, Mp, Np, Kp, P(pa8), P(as8), P(w8), P(s8), P(c8), Np, 1, P(t1))
+
+    one_gemm()
+    ptimes = []
+    t_end = time.perf_counter() + budget_s / 4
+    while time.perf_counter() < t_end or len(ptimes) < 5:
+        t0 = time.perf_counter()
+        one_gemm()
+        ptimes.append(time.perf_counter() - t0)
     L.orc_pool_stop()
+    pmed = sorted(ptimes)[len(ptimes) // 2]
     med = sorted(times)[len(times) // 2]
     step_bytes = (gemm_bytes(4, 8, 8192, 2048) + gemm_bytes(4, 8, 2048, 8192)
                   + prep_bytes(8, 2048) + prep_bytes(8, 8192))
@@ -701,11 +741,32 @@ def cpu_baseline(host, budget_s=10.0):
     except OSError:
         pass
     amx = bool(R is not None and R.fgm_cpu_has_amx())
+    phys, smt = cpu_topology()
     return {"value": step_bytes / med / 1e9, "unit": "GB/s", "cores": nt, "kind": kind,
+            "physical_cores": phys, "smt_used": smt,
             "sample": f"{len(times)} steps of cfg2 (prep + q4g up + prep + q4g down, M=8) in "
                       f"~{budget_s:.0f} s, median step {med * 1e3:.3f} ms; reference "
-                      f"fgm_prep_rows + fgm_gemm_q4g_vnni, pool.rs N-split over {nt} threads; "
-                      f"host '{cpu}', AMX present: {amx} (AMX path not timed)"}
+                      f"fgm_prep_rows + fgm_gemm_q4g_vnni, pool.rs N-split over {nt} threads "
+                      f"({phys} physical cores, SMT {'used' if smt else 'not used'}); "
+                      f"host '{cpu}', AMX present: {amx} (AMX path not timed)",
+            "prefill": {"value": 2.0 * Mp * Np * Kp / pmed / 1e12, "unit": "TOPS",
+                        "sample": f"{len(ptimes)} runs of fgm_gemm_q8c_vnni M={Mp} N={Np} K={Kp} "
+                                  f"(BASELINE configs[2] q) on the same {nt} threads, median "
+                                  f"{pmed * 1e3:.3f} ms"}}
+
+
+def cpu_topology():
+    """(physical cores, SMT used) among the CPUs this process may run on."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else []
+    cores = set()
+    for c in cpus:
+        try:
+            pkg = open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip()
+            core = open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", c))
+    return len(cores), len(cores) < len(cpus)
 
 
 # ------------------------------------------------------------------ main
@@ -731,7 +792,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
-                    help="run one extra measurement (ceilings, cfg1, int4_stream, cfg3, cfg5, cfg4, elem, "
+                    help="run one extra measurement (ceilings, cfg1, int4_stream, cfg3, vendor, cfg5, cfg4, elem, "
                          "prep_fused, attn, model) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -743,7 +804,7 @@ def main():
     gpu = Gpu()
     gpu.t.manual_seed(1234)
     extras = {"ceilings": extra_ceilings, "cfg1": extra_cfg1, "int4_stream": extra_int4_stream,
-              "cfg3": extra_cfg3,
+              "cfg3": extra_cfg3, "vendor": extra_vendor,
               "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem,
               "prep_fused": extra_prep_fused, "attn": extra_attn,
               "model": extra_model}
