@@ -72,6 +72,9 @@ constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thre
 #ifndef FGM_DEC_NWMIN
 #define FGM_DEC_NWMIN 4           // smallest number of stream waves per workgroup
 #endif
+#ifndef FGM_DEC_PIR_MIN_WGS
+#define FGM_DEC_PIR_MIN_WGS 512   // workgroups above which int4 sums are parked in the ring
+#endif
 
 // Two 16-byte LDS reads by byte address, and waits for all but the last six
 // LDS operations (or for all of them) that also order the use of the given
@@ -82,6 +85,24 @@ FGM_DEV void lds_read2x128(v4i& r0, v4i& r1, uint32_t a0, uint32_t a1) {
                : "=&v"(r0), "=&v"(r1)
                : "v"(a0), "v"(a1), "n"(OFF)
                : "memory");
+}
+typedef int v2i __attribute__((ext_vector_type(2)));
+// One group of the parked-in-ring chain: four parked pairs 1 KB apart and
+// their eight scales, six LDS reads; waits for all but the last group read.
+FGM_DEV void pir_read(v2i (&p)[4], v4i (&sc)[2], uint32_t pa, uint32_t sa) {
+  asm volatile(
+      "ds_read_b64 %0, %6\n\tds_read_b64 %1, %6 offset:1024\n\t"
+      "ds_read_b64 %2, %6 offset:2048\n\tds_read_b64 %3, %6 offset:3072\n\t"
+      "ds_read_b128 %4, %7\n\tds_read_b128 %5, %7 offset:16"
+      : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(sc[0]), "=&v"(sc[1])
+      : "v"(pa), "v"(sa)
+      : "memory");
+}
+FGM_DEV void pir_wait6(v2i (&p)[4], v4i (&sc)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(sc[0]), "+v"(sc[1]) : : "memory");
+}
+FGM_DEV void pir_wait0(v2i (&p)[4], v4i (&sc)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(sc[0]), "+v"(sc[1]) : : "memory");
 }
 FGM_DEV void lgkm_wait6(v4i& r0, v4i& r1) {
   asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(r0), "+v"(r1) : : "memory");
@@ -123,11 +144,14 @@ struct Geo {
 // kernel: the weight rings (also the q8c reduction area afterwards), then
 // (int4) the parked tile sums of every k-tile ([n-block][output][k-tile],
 // pitch pp) and the group scales ([n-block][column][group], pitch ngp, zero
-// past the last group); then the epilogue scales.
+// past the last group); then the epilogue scales.  With the park in the ring
+// (pir) the tile sums go back into the slot their weights came from and the
+// park area is empty.
 struct Lay {
   uint32_t ring, park, scl, asc, bsc, total;
   int slots, pp, ngp;
-  __host__ __device__ Lay(int bits, int out, int d, int ks, int upw, int nws, int nbw, int kb, int mp) {
+  __host__ __device__ Lay(int bits, int out, int d, int ks, int upw, int nws, int nbw, int kb, int mp,
+                          bool pir = false) {
     const int tpu = bits == 4 ? 2 : 1;
     slots = upw < d ? upw : d;
     ring = 0;
@@ -137,20 +161,26 @@ struct Lay {
     pp = pitch4(tpu * ks * upw);
     ngp = pitch4((kb + 3) / 4 * 4);
     park = o;
-    o += bits == 4 ? (uint32_t)nbw * out * pp * 4 : 0;
+    o += (bits == 4 && !pir) ? (uint32_t)nbw * out * pp * 4 : 0;
     scl = o;
     o += bits == 4 ? (uint32_t)nbw * 16 * ngp * 4 : 0;
     asc = o;
     o += (uint32_t)(mp + 3) / 4 * 16;
     bsc = o;
     o += (uint32_t)nbw * 64;
+    // pir: the chain's read-ahead may run up to 3 KB past the ring and the
+    // scale rows; keep it inside the workgroup's LDS
+    if (pir) o += 4096;
     total = o;
   }
 };
 
-template <int BITS, int MB, bool HALF, bool G1, bool RAW>
+// PIR: the tile sums are parked in the ring slot their weights came from
+// (int4, M <= 8, group 64, every slot filled once: UPW <= D).
+template <int BITS, int MB, bool HALF, bool G1, bool RAW, bool PIR = false>
 __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   using G = Geo<BITS, MB, HALF>;
+  static_assert(!PIR || (BITS == 4 && HALF && G1 && !RAW), "park in ring: int4, M <= 8, group 64");
   constexpr int TPU = G::TPU, OUT = G::OUT, NA = G::NA, X = G::X, D = G::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick_problem(bt);
@@ -165,7 +195,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   const int Mp = HALF ? 8 : 16 * MB;
   const int nb_first = a.n0 + (int)(blockIdx.x - a.wg0) * NBW;
   const int nb_here = min(NBW, a.n0 + a.nblocks - nb_first);
-  const Lay L(BITS, OUT, D, KS, UPW, NWS, NBW, KB, Mp);
+  const Lay L(BITS, OUT, D, KS, UPW, NWS, NBW, KB, Mp, PIR);
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   constexpr uint32_t TB = BITS == 4 ? 512u : 1024u;  // bytes per k-tile
 
@@ -199,7 +229,9 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   v4i af[D][NA];
   auto issue = [&](int u, auto slc) __attribute__((always_inline)) {
     constexpr int sl = decltype(slc)::value;
-    const uint32_t gu = (uint32_t)(u * KS + s);    // unit index in the n-block
+    // unit index in the n-block: round robin over the KS waves, or (PIR)
+    // a contiguous run per wave, so that the parked pairs lie in k order
+    const uint32_t gu = PIR ? (uint32_t)(s * UPW + u) : (uint32_t)(u * KS + s);
     dma16<true>(rb, ring_w + sl * 1024, bsw, gu * 1024u);
 #pragma unroll
     for (int x = 0; x < NA; x++) af[sl][x] = buf_load_b128(ra, avoff[x], gu * TPU * 1024u);
@@ -253,7 +285,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   // zero here -- LDS left by an earlier workgroup may hold any bits, a NaN
   // among them, and 0 * NaN would reach the output.  The barrier before the
   // chain orders these writes.
-  if (BITS == 4 && G1 && !RAW) {
+  if (BITS == 4 && G1 && !RAW && !PIR) {
     const int lo = TR * UPW, hi = ((KB + 3) >> 2) * 4;
     if (hi > lo) {
       float* Pz = (float*)(smem + L.park);
@@ -313,8 +345,11 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
 #pragma unroll
               for (int e = 0; e < TPU; e++) ts[e][mb] = mfma16(af[i][mb * TPU + e], bv[e], v4i{0, 0, 0, 0});
           }
-          // park [n-block][output][k-tile], k-tile TR u + 2 s + e
+          // park [n-block][output][k-tile], k-tile TR u + 2 s + e; PIR: the
+          // slot just read holds [output][e] (its B fragments are in
+          // registers, and no DMA refills it)
           int32_t* P = (int32_t*)(smem + L.park) + (q * OUT) * L.pp + TR * u + 2 * s;
+          float* Pr = (float*)(smem + L.ring + ((size_t)w * L.slots + i) * 1024);
           if (!HALF || g < 2) {
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
@@ -323,7 +358,9 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
                 const int oo = (16 * mb + 4 * g + r) * 16 + j;
                 // group 64: the sum is a whole group's, parked as the float
                 // the chain multiplies (exact: |16 acc| < 2^24)
-                if (G1 && !RAW)
+                if (PIR)
+                  *(float2*)(Pr + 2 * oo) = float2{(float)ts[0][mb][r], (float)ts[1][mb][r]};
+                else if (G1 && !RAW)
                   *(float2*)(P + oo * L.pp) = float2{(float)ts[0][mb][r], (float)ts[1][mb][r]};
                 else
                   *(int2*)(P + oo * L.pp) = int2{ts[0][mb][r], ts[1][mb][r]};
@@ -362,7 +399,45 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
       const int32_t* P = (const int32_t*)(smem + L.park) + (qq * OUT + oo) * L.pp;
       const float* Sc = S + (qq * 16 + c) * L.ngp;
       const int n = (nb_first + qq) * 16 + c;
-      if (G1 && !RAW) {
+      if constexpr (PIR) {
+        // group = k-tile, parked in the ring: wave qq KS + s parked units
+        // s UPW .. s UPW + UPW - 1 in its slots, so pair p (k-tiles 2p,
+        // 2p + 1, 8 bytes per output) lies at 1 KB x p; its scales are floats
+        // 2p, 2p + 1 of the column's row.  Groups of four pairs, read one
+        // group ahead (inline asm, waited for with lgkmcnt); reads past the
+        // last pair stay inside the workgroup's LDS and are not used.
+        const int np = (KB + 1) >> 1, ng = (np + 3) >> 2;
+        uint32_t pb = lds0 + L.ring + (uint32_t)(qq * KS * L.slots) * 1024u + (uint32_t)oo * 8u;
+        uint32_t sb = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
+        float cacc = 0.0f;
+        v2i pv[2][4];
+        v4i sv[2][2];
+        pir_read(pv[0], sv[0], pb, sb);
+        for (int gi = 0; gi < ng; gi += 2) {
+          sfor<0, 2>([&](auto hc) {
+            constexpr int h = decltype(hc)::value;
+            if (gi + h < ng) {
+              if (gi + h + 1 < ng) {
+                pir_read(pv[h ^ 1], sv[h ^ 1], pb + 4096u * (h + 1), sb + 32u * (h + 1));
+                pir_wait6(pv[h], sv[h]);
+              } else {
+                pir_wait0(pv[h], sv[h]);
+              }
+              const int p0 = 4 * (gi + h);
+#pragma unroll
+              for (int b = 0; b < 4; b++)
+                if (p0 + b < np) {
+                  const int sx = sv[h][b >> 1][2 * (b & 1)], sy = sv[h][b >> 1][2 * (b & 1) + 1];
+                  cacc = __builtin_fmaf(__int_as_float(pv[h][b].x), __int_as_float(sx), cacc);
+                  cacc = __builtin_fmaf(__int_as_float(pv[h][b].y), __int_as_float(sy), cacc);
+                }
+            }
+          });
+          pb += 8192u;
+          sb += 64u;
+        }
+        a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
+      } else if (G1 && !RAW) {
         // group = k-tile: chunks of four; the next chunk's sums and scales are
         // read (volatile: kept in place) before this chunk's fmas
         // LDS reads by address (ds_read_b128 in inline asm, waited for with
@@ -452,19 +527,19 @@ void plan_split(int bits, int M, int K, int* ks, int* upw) {
   *upw = (kbu + k - 1) / k;
 }
 
-Lay lay_for(int bits, int M, int K, int ks, int nws, int nbw) {
+Lay lay_for(int bits, int M, int K, int ks, int nws, int nbw, bool pir = false) {
   const int MB = (M + 15) / 16;
   const bool half = M <= 8;
   const int out = half ? 128 : 256 * MB;
   const int tpu = bits == 4 ? 2 : 1;
   const int upw = ((K / 64 + tpu - 1) / tpu + ks - 1) / ks;
-  return Lay(bits, out, ring_depth(bits, MB, half), ks, upw, nws, nbw, K / 64, half ? 8 : 16 * MB);
+  return Lay(bits, out, ring_depth(bits, MB, half), ks, upw, nws, nbw, K / 64, half ? 8 : 16 * MB, pir);
 }
 
 // Does one problem fit a workgroup of nws waves with nbw n-blocks?
-bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw) {
+bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw, bool pir = false) {
   if (ks * nbw > nws || nws > MAX_WAVES) return false;
-  const Lay L = lay_for(bits, M, K, ks, nws, nbw);
+  const Lay L = lay_for(bits, M, K, ks, nws, nbw, pir);
   if (bits == 4) {
     // the group-scale prefetch covers every padded group slot
     if (8 * nbw * L.ngp > SPT * 64 * nws) return false;
@@ -477,9 +552,9 @@ bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw) {
   return L.total <= 160 * 1024;
 }
 
-template <int BITS, int MB, bool HALF, bool G1, bool RAW>
+template <int BITS, int MB, bool HALF, bool G1, bool RAW, bool PIR = false>
 hipError_t launch_variant(const GemmBatch& bt, int nw, size_t lds, int nwg, hipStream_t st) {
-  auto k = decode_kernel<BITS, MB, HALF, G1, RAW>;
+  auto k = decode_kernel<BITS, MB, HALF, G1, RAW, PIR>;
   static hipError_t attr = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL(k, dim3(nwg), dim3(nw * 64), lds, st, bt);
@@ -487,7 +562,11 @@ hipError_t launch_variant(const GemmBatch& bt, int nw, size_t lds, int nwg, hipS
 }
 
 template <int BITS, int MB, bool HALF>
-hipError_t launch_decode(const GemmBatch& bt, bool g1, bool raw, int nw, size_t lds, int nwg, hipStream_t st) {
+hipError_t launch_decode(const GemmBatch& bt, bool g1, bool raw, bool pir, int nw, size_t lds, int nwg,
+                         hipStream_t st) {
+  if constexpr (BITS == 4 && HALF) {
+    if (pir) return launch_variant<4, 1, true, true, false, true>(bt, nw, lds, nwg, st);
+  }
   if constexpr (BITS == 8) {
     return raw ? launch_variant<BITS, MB, HALF, false, true>(bt, nw, lds, nwg, st)
                : launch_variant<BITS, MB, HALF, false, false>(bt, nw, lds, nwg, st);
@@ -559,17 +638,32 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   }
   const bool half = MB == 1 && Mmax <= 8;
   const int Mv = half ? 8 : 16 * MB;  // the variant's row blocking
+  const bool g1 = bits == 4 && bt.p[0].group == 64;
+  const bool raw = bt.p[0].acc_out != nullptr;
+  // The tile sums go back into the ring when every slot is filled once --
+  // and only for grids of several rounds of workgroups, where the smaller
+  // LDS footprint buys occupancy (134 MB int4 stream: 37.6 -> 32.8 us).  A
+  // one-round grid keeps the park area and the round-robin unit order (the
+  // cfg2 pair: 7.75 us, 9.3 us with the park in the ring).
+  bool pir = bits == 4 && half && g1 && !raw;
+  long nwg_plain = 0;
+  for (int i = 0; i < bt.count; i++) {
+    const GemmProb& p = bt.p[i];
+    pir = pir && p.tw <= ring_depth(4, 1, true);
+    nwg_plain += (p.nblocks + NWS / p.ks - 1) / (NWS / p.ks);
+  }
+  pir = pir && nwg_plain > FGM_DEC_PIR_MIN_WGS;
   int nwg = 0;
   size_t lds = 0;
   for (int i = 0; i < bt.count; i++) {
     GemmProb& p = bt.p[i];
     int nbw = NWS / p.ks;
-    while (nbw > 1 && (nbw > p.nblocks || !fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw))) nbw /= 2;
-    if (!fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw)) return hipErrorInvalidValue;
+    while (nbw > 1 && (nbw > p.nblocks || !fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir))) nbw /= 2;
+    if (!fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir)) return hipErrorInvalidValue;
     p.nbw = nbw;
     p.wg0 = nwg;
     nwg += (p.nblocks + nbw - 1) / nbw;
-    const size_t need = lay_for(bits, Mv, p.K, p.ks, NWS, nbw).total;
+    const size_t need = lay_for(bits, Mv, p.K, p.ks, NWS, nbw, pir).total;
     if (need > lds) lds = need;
   }
   if (nwg == 0) return hipSuccess;
@@ -578,23 +672,21 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   // up to the launch's NWS with idle n-blocks is not needed: every problem
   // uses NBW = NWS / KS unless its n-blocks run out
   const int NW = NWS;
-  const bool g1 = bits == 4 && bt.p[0].group == 64;
-  const bool raw = bt.p[0].acc_out != nullptr;
   if (bits == 8) {
-    if (half) return launch_decode<8, 1, true>(bt, g1, raw, NW, lds, nwg, st);
+    if (half) return launch_decode<8, 1, true>(bt, g1, raw, false, NW, lds, nwg, st);
     switch (MB) {
-      case 1: return launch_decode<8, 1, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 2: return launch_decode<8, 2, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 3: return launch_decode<8, 3, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 4: return launch_decode<8, 4, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 1: return launch_decode<8, 1, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 2: return launch_decode<8, 2, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 3: return launch_decode<8, 3, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 4: return launch_decode<8, 4, false>(bt, g1, raw, false, NW, lds, nwg, st);
     }
   } else {
-    if (half) return launch_decode<4, 1, true>(bt, g1, raw, NW, lds, nwg, st);
+    if (half) return launch_decode<4, 1, true>(bt, g1, raw, pir, NW, lds, nwg, st);
     switch (MB) {
-      case 1: return launch_decode<4, 1, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 2: return launch_decode<4, 2, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 3: return launch_decode<4, 3, false>(bt, g1, raw, NW, lds, nwg, st);
-      case 4: return launch_decode<4, 4, false>(bt, g1, raw, NW, lds, nwg, st);
+      case 1: return launch_decode<4, 1, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 2: return launch_decode<4, 2, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 3: return launch_decode<4, 3, false>(bt, g1, raw, false, NW, lds, nwg, st);
+      case 4: return launch_decode<4, 4, false>(bt, g1, raw, false, NW, lds, nwg, st);
     }
   }
   return hipErrorInvalidValue;
