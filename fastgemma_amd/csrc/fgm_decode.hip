@@ -73,7 +73,7 @@ constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thre
 #define FGM_DEC_NWMIN 4           // smallest number of stream waves per workgroup
 #endif
 #ifndef FGM_DEC_PIR_MIN_WGS
-#define FGM_DEC_PIR_MIN_WGS 512   // workgroups above which int4 sums are parked in the ring
+#define FGM_DEC_PIR_MIN_WGS 2048  // workgroups above which int4 sums are parked in the ring
 #endif
 
 // Two 16-byte LDS reads by byte address, and waits for all but the last six
@@ -641,10 +641,11 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   const bool g1 = bits == 4 && bt.p[0].group == 64;
   const bool raw = bt.p[0].acc_out != nullptr;
   // The tile sums go back into the ring when every slot is filled once --
-  // and only for grids of several rounds of workgroups, where the smaller
-  // LDS footprint buys occupancy (134 MB int4 stream: 37.6 -> 32.8 us).  A
-  // one-round grid keeps the park area and the round-robin unit order (the
-  // cfg2 pair: 7.75 us, 9.3 us with the park in the ring).
+  // and only for grids of many rounds of workgroups, where the smaller LDS
+  // footprint buys occupancy (134 MB int4 stream, 8192 workgroups: 37.6 ->
+  // 32.8 us).  Smaller grids keep the park area and the round-robin unit
+  // order (the cfg2 pair, 256 workgroups: 7.75 us, 9.3 us with the park in
+  // the ring; the cfg4 gate/up batch, 1024: 8.3 us, 8.8 us).
   bool pir = bits == 4 && half && g1 && !raw;
   long nwg_plain = 0;
   for (int i = 0; i < bt.count; i++) {

@@ -1,7 +1,7 @@
 """The skinny kernel's park-in-ring variant (int4, M <= 8, group 64, grids of
-more than 512 workgroups): the tile sums go back into the ring slot their
+more than 2048 workgroups): the tile sums go back into the ring slot their
 weights came from and each wave streams a contiguous run of units.  Every
-shape below yields more than 512 workgroups, so the variant runs; the bytes
+shape below yields 4096 or more workgroups, so the variant runs; the bytes
 must equal the oracle's gemm_q4g (vnni_gemm.c:291-322 restated), tolerance 0,
 and the untouched columns stay untouched."""
 from __future__ import annotations
@@ -33,11 +33,11 @@ def same(a, b):
     return np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-# (M, N, K): 1024 workgroups at K = 2048 (4 stream waves) and K = 8192 (16),
+# (M, N, K): 4096 workgroups at K = 2048 (4 stream waves) and K = 8192 (16),
 # an odd k-tile count (K = 576), two k-tiles (K = 128), one (K = 64),
 # every row count
-CASES = [(8, 16384, 2048), (8, 16384, 8192), (5, 32768, 576), (3, 32768, 1024), (1, 16384, 2048),
-         (8, 65536, 128), (7, 65536, 64), (2, 16384, 4096)]
+CASES = [(8, 65536, 2048), (8, 65536, 8192), (5, 131072, 576), (3, 131072, 1024), (1, 65536, 2048),
+         (8, 262144, 128), (7, 262144, 64), (2, 65536, 4096)]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"m{c[0]}_n{c[1]}_k{c[2]}" for c in CASES])
@@ -49,13 +49,13 @@ def test_park_in_ring_matches_oracle(case):
 
 def test_park_in_ring_n_range():
     """A column range inside a large grid: only [16 n0, 16 n1) is written."""
-    got, want = run(8, 32768, 2048, seed=5, n0=100, n1=1900)
+    got, want = run(8, 131072, 2048, seed=5, n0=100, n1=7000)
     assert same(got, want)
-    assert np.all(got[:, :1600] == -9.0) and np.all(got[:, 1900 * 16:] == -9.0)
+    assert np.all(got[:, :1600] == -9.0) and np.all(got[:, 7000 * 16:] == -9.0)
 
 
 def test_park_in_ring_batch_gate_up():
-    """gate and up of the cfg4 layer in one launch (1024 workgroups)."""
+    """Two up-projection-like problems in one launch (4096 workgroups)."""
     from fastgemma_amd import kernels as K
     t = H.torch()
     outs, wants, probs = [], [], []
@@ -63,15 +63,16 @@ def test_park_in_ring_batch_gate_up():
     Ap = oracle.pack_a(8, 2048, A)
     a_s = oracle.gen_uniform(32, 8, 1e-3, 1e-2)
     dA, das = H.dev(Ap), H.dev(a_s)
+    N = 32768
     for i in range(2):
-        B = oracle.gen_u8(40 + i, 8192 * 1024)
-        bs = oracle.gen_uniform(50 + i, 32 * 8192, 5e-3, 5e-2).astype(np.float16).view(np.uint16)
-        c = t.full((8, 8192), -9.0, dtype=t.float32, device="cuda")
+        B = oracle.gen_u8(40 + i, N * 1024)
+        bs = oracle.gen_uniform(50 + i, 32 * N, 5e-3, 5e-2).astype(np.float16).view(np.uint16)
+        c = t.full((8, N), -9.0, dtype=t.float32, device="cuda")
         outs.append(c)
-        probs.append(dict(bits=4, m=8, n=8192, k=2048, a=dA, a_scale=das, b=H.dev(B), b_scale=H.dev(bs),
-                          c=c, ldc=8192, n0=0, n1=512, group=64))
-        w = np.full((8, 8192), -9.0, np.float32)
-        oracle.gemm_q4g(8, 8192, 2048, Ap, a_s, B, bs.reshape(32, 8192), 64, w, 8192, 0, 512)
+        probs.append(dict(bits=4, m=8, n=N, k=2048, a=dA, a_scale=das, b=H.dev(B), b_scale=H.dev(bs),
+                          c=c, ldc=N, n0=0, n1=N // 16, group=64))
+        w = np.full((8, N), -9.0, np.float32)
+        oracle.gemm_q4g(8, N, 2048, Ap, a_s, B, bs.reshape(32, N), 64, w, N, 0, N // 16)
         wants.append(w)
     K.gemm_batch(probs)
     for c, w in zip(outs, wants):
