@@ -238,6 +238,13 @@ LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048
          ("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
 
 
+def attainable(bits, M, N, K, group=64):
+    """min(peak, AI x 8 TB/s) for one GEMM: AI = 2 M N K ops over the bytes it
+    must move at least once (weights + scales + packed A + a_scale + f32 C)."""
+    ai = 2.0 * M * N * K / gemm_bytes(bits, M, N, K, group)
+    return min(I8_PEAK, ai * HBM_PEAK)
+
+
 def extra_cfg3(gpu):
     ncp = 5                                         # 5 x 58 MB of int8 layers > MALL
     res, tot_ops, tot_t = {}, 0.0, 0.0
@@ -250,7 +257,8 @@ def extra_cfg3(gpu):
         c = gpu.t.empty(256, N, device=gpu.dev)
         dt = kernel_avg(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[i % ncp][0], ws[i % ncp][1], c), 20)
         ops = 2.0 * 256 * N * K
-        res[name] = {"us": dt * 1e6, "TOPS": ops / dt / 1e12, "frac_mfma": ops / dt / I8_PEAK}
+        res[name] = {"us": dt * 1e6, "TOPS": ops / dt / 1e12, "frac_mfma": ops / dt / I8_PEAK,
+                     "frac_attainable": ops / dt / attainable(8, 256, N, K)}
         tot_ops += ops
         tot_t += dt
         del ws
@@ -353,7 +361,8 @@ def extra_cfg5(gpu):
         dt = kernel_avg(gpu, fn, 8, 3)
         ops = 2.0 * 2048 * N * K
         res[name] = {"bits": bits, "us": dt * 1e6, "TOPS": ops / dt / 1e12,
-                     "frac_mfma": ops / dt / I8_PEAK}
+                     "frac_mfma": ops / dt / I8_PEAK,
+                     "frac_attainable": ops / dt / attainable(bits, 2048, N, K)}
     return {"workload": "long prefill M=2048 (gate/up int4 g64, down int8)", "per_shape": res}
 
 
