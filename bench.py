@@ -626,12 +626,18 @@ def extra_model(gpu):
     with tempfile.TemporaryDirectory() as d:
         path = d + "/bench.fgm"
         write_fgm(path, {"hidden_size": 2048}, tensors)
-        t0 = time.perf_counter()
-        m = Model(path, resident=True)
-        t.cuda.synchronize()
-        open_s = time.perf_counter() - t0
-        res["open_resident"] = {"s": open_s, "bytes": m.total_bytes(),
-                                "GB_s": m.total_bytes() / open_s / 1e9}
+        # the first resident open of a process includes one-time runtime set-up
+        # (upload stream, pinned staging); the second is the steady upload rate
+        opens = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            m = Model(path, resident=True)
+            t.cuda.synchronize()
+            opens.append(time.perf_counter() - t0)
+            if len(opens) < 2:
+                m.close()
+        res["open_resident"] = {"s": opens[1], "first_open_s": opens[0], "bytes": m.total_bytes(),
+                                "GB_s": m.total_bytes() / opens[1] / 1e9}
         sel = Selection.parse("auto:16")
         for rows in (8, 256):
             w = m.dual("up").pick(rows, sel)

@@ -434,6 +434,18 @@ int check_prep(const fgm_hip_prep_desc& d) {
 
 }  // namespace
 
+// The calling thread's drop-in staging for the other sources' drop-ins
+// (fgm_model.hip): its stream, a device buffer and a pinned host buffer of
+// at least the given sizes (slots of their own, valid until the thread's
+// next staging request).
+int fgm_stage(size_t dev_bytes, size_t pin_bytes, void** dev, void** pin, hipStream_t* st) {
+  int rc = staging(5, dev_bytes, dev);
+  if (rc || (rc = pinned(0, pin_bytes, pin))) return rc;
+  *st = g_stage.st;
+  return FGM_HIP_OK;
+}
+
+
 // ====================================================================== C ABI
 // Status helpers for the library's other sources (fgm_model.hip).
 int fgm_status_fail(int code, const char* msg) { return fail(code, "%s", msg); }

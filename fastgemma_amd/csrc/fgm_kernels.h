@@ -74,6 +74,10 @@ struct PrepBatch {
   int count;
 };
 
+// The calling thread's drop-in staging (fgm_api.hip): its stream, a device
+// and a pinned host buffer of at least the given sizes; status as the C ABI.
+int fgm_stage(size_t dev_bytes, size_t pin_bytes, void** dev, void** pin, hipStream_t* st);
+
 // Every problem of a batch has the same preop; a preop needs k % 64 == 0 (no
 // scalar tails).
 hipError_t fgm_launch_prep(const PrepBatch& b, hipStream_t st);

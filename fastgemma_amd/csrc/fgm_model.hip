@@ -309,6 +309,46 @@ void json_dump(const Json& v, std::string& o) {
   }
 }
 
+// The tensor body from the file to HBM through two pinned 8 MiB buffers:
+// pread fills one (no page faults on the mapping) while the DMA engine
+// drains the other.
+int upload_body(void* dev, int fd, size_t file_off, size_t n) {
+  constexpr size_t CH = (size_t)8 << 20;
+  void* pin[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  hipStream_t st = nullptr;
+  hipError_t e = hipSuccess;
+  int rc = FGM_HIP_OK;
+  if ((e = hipStreamCreate(&st)) != hipSuccess) return hip_fail(e, "model: upload stream");
+  for (int i = 0; i < 2 && e == hipSuccess; i++) {
+    if ((e = hipHostMalloc(&pin[i], CH, hipHostMallocDefault)) == hipSuccess) e = hipEventCreate(&done[i]);
+  }
+  for (size_t off = 0, c = 0; e == hipSuccess && off < n; off += CH, c ^= 1) {
+    const size_t len = n - off < CH ? n - off : CH;
+    if ((e = hipEventSynchronize(done[c])) != hipSuccess) break;  // the buffer's last copy is done
+    for (size_t got = 0; got < len;) {
+      const ssize_t r = pread(fd, (uint8_t*)pin[c] + got, len - got, (off_t)(file_off + off + got));
+      if (r <= 0) {
+        rc = fail(FGM_HIP_EINVAL, "model: read failed at offset %zu", file_off + off + got);
+        break;
+      }
+      got += (size_t)r;
+    }
+    if (rc) break;
+    if ((e = hipMemcpyAsync((uint8_t*)dev + off, pin[c], len, hipMemcpyHostToDevice, st)) != hipSuccess) break;
+    e = hipEventRecord(done[c], st);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  else (void)hipStreamSynchronize(st);
+  if (e != hipSuccess && !rc) rc = hip_fail(e, "model: upload");
+  for (int i = 0; i < 2; i++) {
+    if (done[i]) (void)hipEventDestroy(done[i]);
+    if (pin[i]) (void)hipHostFree(pin[i]);
+  }
+  (void)hipStreamDestroy(st);
+  return rc;
+}
+
 int open_model(const char* path, int resident, fgm_hip_model** out) {
   std::unique_ptr<fgm_hip_model> m(new fgm_hip_model());
   m->fd = open(path, O_RDONLY);
@@ -373,8 +413,7 @@ int open_model(const char* path, int resident, fgm_hip_model** out) {
       m->dev = nullptr;
       return hip_fail(e, "model: device allocation");
     }
-    if ((e = hipMemcpy(m->dev, b + m->body_lo, n, hipMemcpyHostToDevice)) != hipSuccess)
-      return hip_fail(e, "model: upload");
+    if ((rc = upload_body(m->dev, m->fd, m->body_lo, n))) return rc;
   }
   *out = m.release();
   return FGM_HIP_OK;
@@ -608,23 +647,27 @@ static int dropin_gather(int bits, float* out, const void* tbl, const void* sc, 
   const size_t sb = bits == 8 ? 4 : (size_t)(k / 64) * 2;
   const uint8_t* trow = (const uint8_t*)tbl + (size_t)row * rb;
   const uint8_t* srow = (const uint8_t*)sc + (size_t)row * sb;
-  void *dt = nullptr, *ds = nullptr, *dout = nullptr;
+  // in: [row | scales] through pinned memory, out: the k floats, one copy
+  // each way on the thread's staging stream, no allocation per call
+  const size_t so = (rb + 255) & ~(size_t)255, oo = (so + sb + 255) & ~(size_t)255;
+  const size_t pinb = oo > (size_t)k * 4 ? oo : (size_t)k * 4;
+  void *dbuf = nullptr, *pin = nullptr;
+  hipStream_t st = nullptr;
+  if ((rc = fgm_stage(oo + (size_t)k * 4, pinb, &dbuf, &pin, &st))) return rc;
+  memcpy(pin, trow, rb);
+  memcpy((char*)pin + so, srow, sb);
   hipError_t e;
-  if ((e = hipMalloc(&dt, rb)) != hipSuccess || (e = hipMalloc(&ds, sb)) != hipSuccess ||
-      (e = hipMalloc(&dout, (size_t)k * 4)) != hipSuccess) {
-    (void)hipFree(dt), (void)hipFree(ds);
-    return hip_fail(e, "gather: staging");
-  }
-  rc = FGM_HIP_OK;
-  if ((e = hipMemcpy(dt, trow, rb, hipMemcpyHostToDevice)) != hipSuccess ||
-      (e = hipMemcpy(ds, srow, sb, hipMemcpyHostToDevice)) != hipSuccess)
-    rc = hip_fail(e, "gather: upload");
+  if ((e = hipMemcpyAsync(dbuf, pin, so + sb, hipMemcpyHostToDevice, st)) != hipSuccess)
+    return hip_fail(e, "gather: upload");
   // the staged row is row 0 of a one-row table
-  if (!rc) rc = gather_launch(bits == 8 ? "q8r" : "q4r", (float*)dout, dt, ds, nullptr, 0, 1, k, nullptr);
-  if (!rc && (e = hipMemcpy(out, dout, (size_t)k * 4, hipMemcpyDeviceToHost)) != hipSuccess)
-    rc = hip_fail(e, "gather: download");
-  (void)hipFree(dt), (void)hipFree(ds), (void)hipFree(dout);
-  return rc;
+  float* dout = (float*)((char*)dbuf + oo);
+  rc = gather_launch(bits == 8 ? "q8r" : "q4r", dout, dbuf, (char*)dbuf + so, nullptr, 0, 1, k, st);
+  if (rc) return rc;
+  if ((e = hipMemcpyAsync(pin, dout, (size_t)k * 4, hipMemcpyDeviceToHost, st)) != hipSuccess ||
+      (e = hipStreamSynchronize(st)) != hipSuccess)
+    return hip_fail(e, "gather: download");
+  memcpy(out, pin, (size_t)k * 4);
+  return FGM_HIP_OK;
 }
 
 // ------------------------------------------------------- the pool's jobs
