@@ -359,6 +359,32 @@ def gemm_q4g(m, n, k, ap, a_scale, bq, b_scale, group, c, ldc, n0, n1) -> None:
                        _ptr(c), ldc, n0, n1)
 
 
+def gemm_pooled(bits, m, n, k, ap, a_scale, b, b_scale, group, c, ldc, use_ref=True) -> str:
+    """gemm_q8c / gemm_q4g over all of [0, n/16), split across host threads
+    the way fgm-core's pool splits a GEMM (cpu_pool.c, pool.rs:110-145): the
+    reference's own VNNI kernels when oracle/_ref is built and the host has
+    AVX-512 VNNI (use_ref), else the oracle's scalar restatement.  Columns are
+    independent, so the bytes equal one call over the whole range.  Returns
+    which ran ("reference" / "oracle")."""
+    L = lib()
+    R = ref() if use_ref else None
+    nt = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    L.orc_pool_start(max(1, min(nt, 64)))
+    t1 = np.empty(1, np.float64)
+    try:
+        if bits == 8:
+            fn = C.cast(R.fgm_gemm_q8c_vnni if R is not None else L.orc_gemm_q8c, C.c_void_p).value
+            L.orc_pool_q8c(fn, m, n, k, _ptr(ap), _ptr(a_scale), _ptr(b), _ptr(b_scale), _ptr(c), ldc, 1,
+                           _ptr(t1))
+        else:
+            fn = C.cast(R.fgm_gemm_q4g_vnni if R is not None else L.orc_gemm_q4g, C.c_void_p).value
+            L.orc_pool_q4g(fn, m, n, k, _ptr(ap), _ptr(a_scale), _ptr(b), _ptr(b_scale), group, _ptr(c),
+                           ldc, 1, _ptr(t1))
+    finally:
+        L.orc_pool_stop()
+    return "reference" if R is not None else "oracle"
+
+
 # ------------------------------------------------------- elementwise ops
 # Restatements of ops.c's f32 primitives (fgm_oracle.c cites the lines).  All
 # take and return numpy float32 arrays; the in-place reference functions get

@@ -378,3 +378,29 @@ def test_quant_act_live_vs_reference_heavy_tails():
     rs = np.empty_like(s)
     R.fgm_quant_act(P(x), rows, k, P(rq), P(rs))
     assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_pooled_gemm_equals_single_call(bits):
+    """oracle.gemm_pooled (the N-split over host threads the GPU tests use as
+    a full-range checker) gives the single-threaded oracle's bytes, with the
+    oracle and, where oracle/_ref is built, with the reference's kernels."""
+    M, N, K = 24, 1024, 1024
+    A = oracle.gen_i8(71, M * K, -127, 127).reshape(M, K)
+    Ap = oracle.pack_a(M, K, A)
+    s = oracle.gen_uniform(72, M, 1e-3, 1e-2)
+    if bits == 8:
+        B = oracle.gen_i8(73, N * K, -127, 127)
+        bs = oracle.gen_uniform(74, N, 1e-3, 1e-2)
+    else:
+        B = oracle.gen_u8(73, N * K // 2)
+        bs = oracle.gen_uniform(74, (K // 64) * N, 5e-3, 5e-2).astype(np.float16).view(np.uint16)
+    want = np.zeros((M, N), np.float32)
+    if bits == 8:
+        oracle.gemm_q8c(M, N, K, Ap, s, B, bs, want, N, 0, N // 16)
+    else:
+        oracle.gemm_q4g(M, N, K, Ap, s, B, bs, 64, want, N, 0, N // 16)
+    for use_ref in (False, True):
+        got = np.zeros((M, N), np.float32)
+        oracle.gemm_pooled(bits, M, N, K, Ap, s, B, bs, 64, got, N, use_ref=use_ref)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), use_ref
