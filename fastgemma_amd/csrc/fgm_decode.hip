@@ -168,9 +168,14 @@ struct Lay {
     o += (uint32_t)(mp + 3) / 4 * 16;
     bsc = o;
     o += (uint32_t)nbw * 64;
-    // pir: the chain's read-ahead may run up to 3 KB past the ring and the
-    // scale rows; keep it inside the workgroup's LDS
-    if (pir) o += 4096;
+    // pir: the chain's last group of pair reads may run up to 3 KB past the
+    // ring (and its scale reads 32 bytes past the scale rows); the areas
+    // after the ring absorb most of it, pad the rest so the reads stay inside
+    // the workgroup's LDS
+    if (pir) {
+      const uint32_t ring_end = (uint32_t)nws * slots * 1024, need = ring_end + 3072 + 32;
+      if (o < need) o = need;
+    }
     total = o;
   }
 };
