@@ -125,3 +125,32 @@ def test_pool_jobs_equal_linear_run(model):
     out = t.zeros((m, w.n), dtype=t.float32, device="cuda")
     linear_run(w, a, m, w.k, out)
     assert np.array_equal(H.host(c).view(np.uint32), H.host(out).view(np.uint32))
+
+
+def test_reference_written_file_on_the_gpu():
+    """The file written by the reference's own FgmWriter (tests/golden/
+    ref_writer.fgm), resident: Gemm::run through both weights of the dual and
+    both gathers equal the oracle on the file's bytes."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_writer.fgm")
+    t = H.torch()
+    with Model(path, resident=True) as m:
+        for name in ("layers.0.mlp.up", "layers.0.mlp.up.i8"):
+            w = m.linear(name)
+            for rows in (3, 20):
+                a = oracle.gen_student_t(31 + rows, rows * w.k, 3).reshape(rows, w.k)
+                out = t.zeros((rows, w.n), dtype=t.float32, device="cuda")
+                linear_run(w, H.dev(a), rows, w.k, out)
+                want = oracle_linear(w, a.ravel(), rows, w.k)
+                assert np.array_equal(H.host(out).view(np.uint32), want.view(np.uint32)), (name, rows)
+        for name, bits in (("embed", 8), ("ple", 4)):
+            shape = m.shape(name)
+            k = shape[1]
+            tbl = m.i8s(name) if bits == 8 else m.u8s(name)
+            sc = m.f32s(name + ".scale") if bits == 8 else m.f16s(name + ".scale").view(np.uint16)
+            rows = [0, shape[0] - 1, 1]
+            want = np.stack([oracle.gather(bits, np.ascontiguousarray(tbl), np.ascontiguousarray(sc).ravel(), r, k)
+                             for r in rows])
+            out = t.zeros((len(rows), k), dtype=t.float32, device="cuda")
+            m.gather(name, t.tensor(rows, dtype=t.int32, device="cuda"), out)
+            assert np.array_equal(H.host(out).view(np.uint32), want.view(np.uint32)), name
