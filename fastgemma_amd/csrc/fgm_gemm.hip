@@ -333,23 +333,33 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   // barrier frees slot sidx, whose refill (stage sidx + NS) starts.  Trips of
   // U2 stages keep the register set of every k-block a constant; k-blocks
   // past K hold zeros.
+  // One trip covers UR stages, a whole number of ring rounds (and an even
+  // number of k-blocks, so the register set of every k-block is a constant):
+  // every stage's ring slot is then a constant too and its fragment
+  // addresses fold into the reads' immediate offsets instead of being
+  // recomputed per stage.  Stages past the last one holding k-blocks of K
+  // are skipped (the condition is the same for every wave of the workgroup).
   constexpr int U2 = KS % 2 == 0 ? 1 : 2;
-  const int NSTG = (KB + KS * KW * U2 - 1) / (KS * KW * U2) * U2;
-  for (int sb = 0; sb < NSTG; sb += U2) {
-    sfor<0, U2 * KS>([&](auto ic) {
+  constexpr int UR = NS % U2 == 0 ? NS : (U2 % NS == 0 ? U2 : NS * U2);
+  const int NSTG = (KB + KS * KW - 1) / (KS * KW);
+  for (int sb = 0; sb < NSTG; sb += UR) {
+    sfor<0, UR * KS>([&](auto ic) {
       constexpr int i = decltype(ic)::value, u = i / KS, j = i % KS, cur = i & 1;
-      const int sidx = sb + u, kb = (sidx * KW + kg) * KS + j;
-      const bool fresh = BITS == 4 && (kb % gk) == 0;
-      if constexpr (j + 1 < KS) {
-        mma(std::integral_constant<int, cur>{}, fresh, sidx - 1 + NS, (sidx + NS - 1) % NS, j + 1,
-            gring + (sidx % NS) * C::STAGE + (j + 1) * C::KBLK);
-      } else {
-        wait_vm<(NS - 2) * C::U>();
-        __syncthreads();
-        mma(std::integral_constant<int, cur>{}, fresh, sidx + NS, sidx % NS, 0,
-            gring + ((sidx + 1) % NS) * C::STAGE);
+      constexpr int slot = u % NS, prev = (u + NS - 1) % NS, next = (u + 1) % NS;
+      const int sidx = sb + u;
+      if (sidx < NSTG) {
+        const int kb = (sidx * KW + kg) * KS + j;
+        const bool fresh = BITS == 4 && (kb % gk) == 0;
+        if constexpr (j + 1 < KS) {
+          mma(std::integral_constant<int, cur>{}, fresh, sidx - 1 + NS, prev, j + 1,
+              gring + slot * C::STAGE + (j + 1) * C::KBLK);
+        } else {
+          wait_vm<(NS - 2) * C::U>();
+          __syncthreads();
+          mma(std::integral_constant<int, cur>{}, fresh, sidx + NS, slot, 0, gring + next * C::STAGE);
+        }
+        drain(std::integral_constant<int, cur>{}, kb);
       }
-      drain(std::integral_constant<int, cur>{}, kb);
     });
   }
   wait_vm<0>();
