@@ -198,12 +198,14 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   const int gk = BITS == 4 ? a.group >> 6 : 1;
   const int NG = BITS == 4 ? KB / gk : 0;
   const int Mp = HALF ? 8 : 16 * MB;
-  // Workgroups go round-robin over the 8 XCDs: give each XCD a contiguous
-  // run of n-blocks, so that the workgroups sharing a 128-byte line of int4
-  // group scales (four n-blocks) share an L2 and fetch it from HBM once.
+  // Workgroups go round-robin over the 8 XCDs: for int4, give each XCD a
+  // contiguous run of n-blocks, so that the workgroups sharing a 128-byte
+  // line of group scales (four n-blocks) share an L2 and fetch it from HBM
+  // once.  (int8 scales are one float per column, nothing is shared, and
+  // the interleaved order measured faster: cfg1 5.45 against 6.3 us.)
   int lb = (int)blockIdx.x - a.wg0;
   const int nwgp = (a.nblocks + NBW - 1) / NBW;
-  if ((a.wg0 & 7) == 0 && (nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
+  if (BITS == 4 && (a.wg0 & 7) == 0 && (nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
   const int nb_first = a.n0 + lb * NBW;
   const int nb_here = min(NBW, a.n0 + a.nblocks - nb_first);
   const Lay L(BITS, OUT, D, KS, UPW, NWS, NBW, KB, Mp, PIR);
