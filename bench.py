@@ -377,6 +377,7 @@ def extra_ceilings(gpu):
     L.fgm_ceil_empty.argtypes = [C.c_int, C.c_int, C.c_void_p]
     L.fgm_ceil_read.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p]
     L.fgm_ceil_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    L.fgm_ceil_read_lds.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     L.fgm_ceil_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
     t = gpu.t
 
@@ -388,22 +389,30 @@ def extra_ceilings(gpu):
     for nwg, thr in ((1, 64), (256, 256), (256, 1024)):
         dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_empty(nwg, thr, gpu.stream())), 64, 5)
         res[f"empty_launch_{nwg}x{thr}_us"] = dt * 1e6
-    chunk = 256 * 16 * 8
+    chunk = 16 * 8 * 1024  # a multiple of every probe's per-workgroup bytes
     sink = t.zeros(600 * 1000 * 1000 // 4096, dtype=t.int32, device=gpu.dev)
     reads = {}
     for mb, copies in ((18, 48), (134, 6), (537, 2)):
         nbytes = (mb * 1000 * 1000) // chunk * chunk
         bufs = [t.empty(nbytes, dtype=t.uint8, device=gpu.dev) for _ in range(copies)]
-        best = None
+        best, best_lds = None, None
         for u in (1, 2, 4, 8):
             dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_read(bufs[i % copies].data_ptr(), nbytes, u,
                                                               sink.data_ptr(), gpu.stream())),
                             max(copies, 8), 3)
             if best is None or dt < best[0]:
-                best = (dt, u)
-        reads[f"{mb}MB"] = {"bytes": nbytes, "us": best[0] * 1e6, "GB_s": nbytes / best[0] / 1e9,
-                            "frac_hbm": nbytes / best[0] / HBM_PEAK,
-                            "bytes_per_workgroup": 4096 * best[1]}
+                best = (dt, f"register loads, {4 * u} KiB per 4-wave workgroup")
+        # the skinny GEMM's path: 1 KB LDS-DMA units, 16-wave workgroups
+        for nw, u in ((16, 4), (16, 2), (16, 8), (8, 8), (8, 4)):
+            dt = kernel_avg(gpu, lambda i: ok(L.fgm_ceil_read_lds(bufs[i % copies].data_ptr(), nbytes, nw, u,
+                                                                  sink.data_ptr(), gpu.stream())),
+                            max(copies, 8), 3)
+            if best_lds is None or dt < best_lds[0]:
+                best_lds = (dt, f"LDS-DMA, {nw} waves x {u} KiB per workgroup")
+        top = min(best, best_lds)
+        reads[f"{mb}MB"] = {"bytes": nbytes, "us": top[0] * 1e6, "GB_s": nbytes / top[0] / 1e9,
+                            "frac_hbm": nbytes / top[0] / HBM_PEAK, "path": top[1],
+                            "register_loads_us": best[0] * 1e6, "lds_dma_us": best_lds[0] * 1e6}
         del bufs
         t.cuda.empty_cache()
     res["read_one_launch"] = reads
