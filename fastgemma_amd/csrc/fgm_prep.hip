@@ -300,8 +300,20 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
-  mx = red[0];
-  for (int w = 1; w < (T >> 6); w++) mx = fmaxf(mx, red[w]);
+  {
+    // every wave's maximum in four 16-byte reads (one LDS round trip), the
+    // slots past the workgroup's waves masked; every maximum is >= 0
+    const int nw = T >> 6;
+    mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < PREP_MAX_THREADS / 256; q++) {
+      const float4 r = *(const float4*)(red + 4 * q);
+      mx = fmaxf(mx, 4 * q + 0 < nw ? r.x : 0.0f);
+      mx = fmaxf(mx, 4 * q + 1 < nw ? r.y : 0.0f);
+      mx = fmaxf(mx, 4 * q + 2 < nw ? r.z : 0.0f);
+      mx = fmaxf(mx, 4 * q + 3 < nw ? r.w : 0.0f);
+    }
+  }
   const float s = (mx == 0.0f) ? 1.0f : mx / 127.0f;
   const float inv = 1.0f / s;
   if (tid == 0) a.qs[row] = s;
@@ -378,7 +390,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
 template <int PRE>
 __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
-  __shared__ float red[PREP_MAX_THREADS / 64];
+  __shared__ __attribute__((aligned(16))) float red[PREP_MAX_THREADS / 64];
   const PrepProb a = pick_problem(bt);
   const int row = a.r0 + (blockIdx.x - a.wg0);
   const int k = a.k, KB = k >> 6;
