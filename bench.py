@@ -49,17 +49,17 @@ def log(*a):
 
 # ------------------------------------------------------------- byte counts
 def gemm_bytes(bits, M, N, K, group=64):
-    """Algorithmic bytes of one GEMM launch: weights + scales + packed A +
-    a_scale + C (fp32).  Packed A counts the rows the layout stores."""
+    """Algorithmic bytes of one GEMM launch: weights + scales + the M rows of
+    int8 A + a_scale + C (fp32).  The packed layout's pad rows (up to the next
+    multiple of 16) carry no data and are not counted."""
     w = N * K if bits == 8 else N * K // 2
     s = N * 4 if bits == 8 else (K // group) * N * 2
-    mp = (M + 15) // 16 * 16
-    return w + s + mp * K + 4 * M + 4 * M * N
+    return w + s + M * K + 4 * M + 4 * M * N
 
 
 def prep_bytes(M, K):
-    mp = (M + 15) // 16 * 16
-    return 4 * M * K + mp * K + 4 * M
+    """fp32 rows read + int8 rows and row scales written."""
+    return 4 * M * K + M * K + 4 * M
 
 
 # ---------------------------------------------------------------- plumbing
