@@ -120,3 +120,36 @@ def test_weight_past_1gib_is_cut_along_n(M):
         oracle.gemm_q8c(M, n, Kd, Ap, a_s, sub, sbs, R, n, 0, n // 16)
         assert _bits_equal(got[:, 16 * nb0:16 * nb1], R), (nb0, nb1)
     del B
+
+
+@pytest.mark.parametrize("kind", ["q8c", "q4g"])
+@pytest.mark.parametrize("M", [256, 96])
+def test_dropin_dense_column_range(kind, M):
+    """Host-pointer drop-ins on the dense kernel with a column range that does
+    not start at 0 (the reference's pool hands each thread [n0, n1),
+    pool.rs:119-145): every written value equals the oracle, the rest of C is
+    untouched.  Regression: the drop-in passes a C base shifted by 16 n0
+    columns, and the dense epilogue's store range once dropped the last row
+    of every tile for such a base."""
+    from fastgemma_amd import kernels as K
+    N, Kd, n0, n1 = 1024, 2048, 12, 44
+    A = oracle.gen_i8(81, M * Kd, -127, 127).reshape(M, Kd)
+    Ap = oracle.pack_a(M, Kd, A)
+    a_s = oracle.gen_uniform(82, M, 1e-3, 1e-2)
+    if kind == "q8c":
+        B = oracle.gen_i8(83, N * Kd, -127, 127)
+        bs = oracle.gen_uniform(84, N, 1e-3, 1e-2)
+    else:
+        B = oracle.gen_u8(83, N * Kd // 2)
+        bs = oracle.gen_uniform(84, (Kd // 64) * N, 5e-3, 5e-2).astype(np.float16).view(np.uint16)
+    C = np.full((M, N), -5.0, np.float32)
+    W = np.full((M, N), -5.0, np.float32)
+    if kind == "q8c":
+        K.gemm_q8c(M, N, Kd, Ap, a_s, B, bs, C, N, n0, n1)
+        oracle.gemm_q8c(M, N, Kd, Ap, a_s, B, bs, W, N, n0, n1)
+    else:
+        K.gemm_q4g(M, N, Kd, Ap, a_s, B, bs, 64, C, N, n0, n1)
+        oracle.gemm_q4g(M, N, Kd, Ap, a_s, B, bs, 64, W, N, n0, n1)
+    assert K.gemm_path(8 if kind == "q8c" else 4, M, Kd) == "dense"
+    assert _bits_equal(C, W)
+    assert np.all(C[:, :16 * n0] == -5.0) and np.all(C[:, 16 * n1:] == -5.0)
