@@ -146,13 +146,21 @@ GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, c
 // skipped; an empty contraction (k == 0) writes 0, as the reference does.
 int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st);
 
+// Bytes of B that a problem's launch addresses: n-blocks [0, n0 + nblocks).
+uint64_t b_span(int bits, const GemmProb& p) {
+  return (uint64_t)(p.n0 + p.nblocks) * (uint64_t)p.K * (bits == 8 ? 16 : 8);
+}
+
 // One problem whose B spans more than FGM_B_CHUNK bytes, as launches over
 // n-block chunks: B, the scales' column, C and acc_out are rebased to the
-// chunk's first column; N stays the scale table's row stride.
+// chunk's first column; N stays the scale table's row stride.  Each chunk
+// starts at n-block 0 of its rebased B and spans at most FGM_B_CHUNK bytes,
+// or is a single n-block (K * 16 bytes < 2^31, as packed A's limit implies:
+// the kernels address it directly), so no chunk is cut again.
 int run_chunked(int bits, const GemmProb& p, hipStream_t st) {
   const uint64_t nb_bytes = (uint64_t)p.K * (bits == 8 ? 16 : 8);
   int step = (int)std::min<uint64_t>(FGM_B_CHUNK / nb_bytes, 1u << 24);
-  if (step < 1) step = 1;  // one n-block of K * 16 bytes: K < 2^27, as packed A's limit implies
+  if (step < 1) step = 1;
   for (int c0 = p.n0; c0 < p.n0 + p.nblocks; c0 += step) {
     GemmProb q = p;
     const int cnt = std::min(step, p.n0 + p.nblocks - c0);
@@ -168,6 +176,12 @@ int run_chunked(int bits, const GemmProb& p, hipStream_t st) {
     if (rc) return rc;
   }
   return FGM_HIP_OK;
+}
+
+// A problem is cut along N when its B span passes FGM_B_CHUNK and a cut can
+// shrink it: a lone n-block at the start of B is launched as it is.
+bool needs_chunks(int bits, const GemmProb& p) {
+  return b_span(bits, p) > FGM_B_CHUNK && (p.n0 > 0 || p.nblocks > 1);
 }
 
 int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
@@ -196,7 +210,7 @@ int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
       continue;
     }
     int rc;
-    if ((uint64_t)(p.n0 + p.nblocks) * (uint64_t)p.K * (bits == 8 ? 16 : 8) > FGM_B_CHUNK) {
+    if (needs_chunks(bits, p)) {
       if ((rc = run_chunked(bits, p, st))) return rc;
       continue;
     }

@@ -153,3 +153,68 @@ def test_dropin_dense_column_range(kind, M):
     assert K.gemm_path(8 if kind == "q8c" else 4, M, Kd) == "dense"
     assert _bits_equal(C, W)
     assert np.all(C[:, :16 * n0] == -5.0) and np.all(C[:, 16 * n1:] == -5.0)
+
+
+@pytest.mark.parametrize("M", [8, 128])
+def test_int4_weight_past_1gib_is_cut_along_n(M):
+    """int4 group 64, N=163840 K=16384 (1.34 GB of weights): launches of at
+    most 2^30 bytes of B (8192 n-blocks each), the f16 scale table rebased by
+    16 columns per n-block with N kept as its row stride; n-blocks at the
+    start, on both sides of the cut and at the end equal the oracle on the
+    same bytes, on the skinny (M=8) and the dense (M=128) kernel."""
+    from fastgemma_amd import kernels as K
+    t = H.torch()
+    N, Kd, G = 163840, 16384, 64
+    print("q4g chunked", M, N, Kd, K.gemm_path(4, M, Kd, G), flush=True)
+    g = t.Generator(device="cuda")
+    g.manual_seed(4321 + M)
+    B = t.randint(0, 256, (N * Kd // 2,), dtype=t.uint8, device="cuda", generator=g)
+    bs = (t.rand((Kd // G) * N, device="cuda", generator=g) * 0.045 + 0.005).half().view(t.int16)
+    A = oracle.gen_i8(65 + M, M * Kd, -127, 127).reshape(M, Kd)
+    Ap = oracle.pack_a(M, Kd, A)
+    a_s = oracle.gen_uniform(66 + M, M, 1e-3, 1e-2)
+    C = t.full((M, N), 3.0, device="cuda")
+    K.gemm_q4g(M, N, Kd, H.dev(Ap), H.dev(a_s), B, bs, G, C, N, 0, N // 16)
+    got = H.host(C)
+    bs_h = H.host(bs).view(np.uint16).reshape(Kd // G, N)
+    for nb0, nb1 in ((0, 4), (8188, 8196), (N // 16 - 4, N // 16)):
+        sub = H.host(B[nb0 * Kd * 8:nb1 * Kd * 8])
+        sbs = np.ascontiguousarray(bs_h[:, 16 * nb0:16 * nb1])
+        n = 16 * (nb1 - nb0)
+        R = np.zeros((M, n), np.float32)
+        oracle.gemm_q4g(M, n, Kd, Ap, a_s, sub, sbs, G, R, n, 0, n // 16)
+        assert _bits_equal(got[:, 16 * nb0:16 * nb1], R), (nb0, nb1)
+    del B
+
+
+def test_single_n_block_past_1gib_launches_whole():
+    """int8, M=8, K = 2^26 + 64: one n-block holds 16 K > 2^30 bytes of B, so
+    every cut along N is a lone n-block, launched as it is (once the cause of
+    an unbounded recursion on the host).  A is zero outside three k-blocks
+    (the first, one in the middle, the last), so the result equals the
+    oracle's on the problem reduced to those k-blocks, bit for bit."""
+    from fastgemma_amd import kernels as K
+    t = H.torch()
+    M, N, Kd = 8, 64, (1 << 26) + 64
+    KB = Kd // 64
+    kbs = [0, KB // 2, KB - 1]
+    print("q8c lone n-block", M, N, Kd, K.gemm_path(8, M, Kd), flush=True)
+    g = t.Generator(device="cuda")
+    g.manual_seed(99)
+    B = t.randint(-127, 128, (N * Kd,), dtype=t.int8, device="cuda", generator=g)
+    bs = oracle.gen_uniform(71, N, 1e-3, 1e-2)
+    a_s = oracle.gen_uniform(72, M, 1e-3, 1e-2)
+    Ar = oracle.gen_i8(73, M * 192, -127, 127).reshape(M, 192)
+    Apr = oracle.pack_a(M, 192, Ar)             # [1][3][16][64]: one 1 KB chunk per k-block
+    Ap = t.zeros(16 * Kd, dtype=t.int8, device="cuda")
+    for i, kb in enumerate(kbs):
+        Ap[kb * 1024:(kb + 1) * 1024] = H.dev(Apr[i * 1024:(i + 1) * 1024])
+    C = t.full((M, N), 3.0, device="cuda")
+    K.gemm_q8c(M, N, Kd, Ap, H.dev(a_s), B, H.dev(bs), C, N, 0, N // 16)
+    got = H.host(C)
+    Br = np.concatenate([H.host(B[(nb * KB + kb) * 1024:(nb * KB + kb + 1) * 1024])
+                         for nb in range(N // 16) for kb in kbs])
+    R = np.zeros((M, N), np.float32)
+    oracle.gemm_q8c(M, N, 192, Apr, a_s, Br, bs, R, N, 0, N // 16)
+    assert _bits_equal(got, R)
+    del B, Ap
