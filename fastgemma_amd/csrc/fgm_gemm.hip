@@ -79,7 +79,7 @@ struct Cfg {
   static_assert(LDS <= 160 * 1024, "LDS per workgroup");
 };
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT>
 __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -152,12 +152,20 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   // this K group's ring
   const uint32_t ring0 = lds0 + (uint32_t)(kg * NS * C::STAGE);
   const char* const gring = smem + kg * NS * C::STAGE;
+  // ROT (int8, whose int32 sum is exact in any k order): workgroup b walks K
+  // from k-block 5 b mod KB, so the tiles that share A rows or B columns read
+  // different k-blocks at a time instead of the same lines at once (M = 256,
+  // N = 2048, K = 8192: 15.7 -> 13.2 us; for M = 2048 the shared lines are
+  // what the L2 reuses, and the rotation doubles the time)
+  static_assert(!ROT || BITS == 8, "k rotation: int8 only");
+  const int rot = ROT ? (int)((uint32_t)bid * 5u % (uint32_t)KB) : 0;
   // loads of k-block j of the group's stage sidx (k-blocks KS * (KW * sidx +
   // kg) ...) into ring slot `slot`; zeros past K, which land in k-blocks that
   // are never multiplied
   auto issue_part = [&](int sidx, int slot, int j) {
-    const int kb = (sidx * KW + kg) * KS + j;
+    int kb = (sidx * KW + kg) * KS + j;
     const bool live = kb < KB;
+    if (ROT && live) kb = kb + rot < KB ? kb + rot : kb + rot - KB;
     const uint32_t sb = ring0 + slot * C::STAGE + j * C::KBLK;
 #pragma unroll
     for (int i = 0; i < UA; i++)
@@ -430,10 +438,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   }
 }
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT>
 hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
-  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, RAW, G1>;
+  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, RAW, G1, ROT>;
   static hipError_t attr =
       hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
   if (attr != hipSuccess) return attr;
@@ -454,13 +462,13 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
 
 // Variant: raw-accumulator dumps or scaled outputs; int4 with 64-wide groups
 // (a fresh accumulator every k-block) or the general group size.
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW = 1>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW = 1, bool ROT = false>
 hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
-  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, true, false>(b, st);
+  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, true, false, ROT>(b, st);
   bool g1 = BITS == 4;
   for (int i = 0; i < b.count; i++) g1 = g1 && b.p[i].group == 64;
-  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, BITS == 4>(b, st)
-            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false>(b, st);
+  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, BITS == 4, ROT>(b, st)
+            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false, ROT>(b, st);
 }
 
 // Shortest K of a batch.
@@ -498,15 +506,18 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // bounded rate (about 16 GB/s per wave from L2 on MI355X), so a small tile
   // needs more waves streaming it, and each group walks a quarter or half of
   // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256;
-  // M = 2048 down, K = 8192: 42.4 -> 38.9 us).
+  // M = 2048 down, K = 8192: 42.4 -> 38.9 us).  Long K keeps more stages in
+  // flight: one k-block per stage, four or five stages per K group (M = 2048
+  // down 34.8 -> 31.0 us; M = 256 down with the k rotation 15.7 -> 13.2 us).
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
     if (tiles(in, 128, 128) >= 240)  // long K (the down projection): two K groups
-      return kmin(in) >= 4096 ? launch_any<8, 2, 2, 2, 2, 2, 2, 2>(in, st)
+      return kmin(in) >= 4096 ? launch_any<8, 2, 2, 2, 2, 4, 1, 2>(in, st)
                               : launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
     if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
     if (tiles(in, 64, 64) >= 160) return launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
-    return launch_any<8, 1, 1, 2, 1, 3, 2, 4>(in, st);
+    return kmin(in) >= 8192 ? launch_any<8, 1, 1, 2, 1, 5, 1, 4, true>(in, st)
+                            : launch_any<8, 1, 1, 2, 1, 3, 2, 4>(in, st);
   }
   if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
   if (tiles(in, 128, 64) >= 240) return launch_any<4, 2, 1, 2, 2, 2, 2>(in, st);
