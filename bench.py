@@ -163,6 +163,11 @@ class Gpu:
         t.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3
 
+    def time_each(self, gs, reps):
+        """Seconds of each of `reps` passes over the graph list, every pass
+        bracketed by synchronize and HIP events on the replay stream."""
+        return [self.time_graphs(gs, 1) for _ in range(reps)]
+
 
 # ------------------------------------------------------------- workloads
 def cfg2_setup(gpu):
@@ -200,11 +205,23 @@ def cfg2_setup(gpu):
     return step, gemv_pair, gemv_up, gemv_down, step_bytes, host
 
 
-def kernel_avg(gpu, fn, n=NCOPY, reps=5):
-    """Average seconds per launch of fn over a graph of n back-to-back launches."""
+def med_range(ts):
+    """(median, min, max) of a list of times."""
+    s = sorted(ts)
+    return s[len(s) // 2], s[0], s[-1]
+
+
+def kernel_time(gpu, fn, n=NCOPY, reps=5):
+    """Seconds per launch of fn, from `reps` timed replays of a graph of n
+    back-to-back launches: (median, min, max) over the replays."""
     gs = gpu.graphs(fn, n, n)
     gpu.time_graphs(gs, 2)
-    return gpu.time_graphs(gs, reps) / (reps * n)
+    return tuple(x / n for x in med_range(gpu.time_each(gs, reps)))
+
+
+def kernel_avg(gpu, fn, n=NCOPY, reps=5):
+    """Median seconds per launch of fn (kernel_time)."""
+    return kernel_time(gpu, fn, n, reps)[0]
 
 
 def extra_cfg1(gpu):
@@ -212,9 +229,10 @@ def extra_cfg1(gpu):
     x, qs, pa = gpu.act(1, 2048)
     c = gpu.t.empty(1, 8192, device=gpu.dev)
     gpu.prep(x, qs, pa, 1, 2048)
-    dt = kernel_avg(gpu, lambda i: gpu.q8c(1, 8192, 2048, pa, qs, ws[i % 24][0], ws[i % 24][1], c), 24)
+    dt, lo, hi = kernel_time(gpu, lambda i: gpu.q8c(1, 8192, 2048, pa, qs, ws[i % 24][0], ws[i % 24][1], c), 24)
     b = gemm_bytes(8, 1, 8192, 2048)
     return {"workload": "int8 GEMV M=1 N=8192 K=2048", "us_per_launch": dt * 1e6,
+            "us_range": [lo * 1e6, hi * 1e6],
             "GB_s": b / dt / 1e9, "frac_hbm": b / dt / HBM_PEAK, "bytes_per_launch": b}
 
 
@@ -228,10 +246,11 @@ def extra_int4_stream(gpu):
     x, qs, pa = gpu.act(8, K)
     gpu.prep(x, qs, pa, 8, K)
     c = gpu.t.empty(8, N, device=gpu.dev)
-    dt = kernel_avg(gpu, lambda i: gpu.q4g(8, N, K, pa, qs, ws[i % 2][0], ws[i % 2][1], c), 8, 3)
+    dt, lo, hi = kernel_time(gpu, lambda i: gpu.q4g(8, N, K, pa, qs, ws[i % 2][0], ws[i % 2][1], c), 8, 5)
     b = gemm_bytes(4, 8, N, K)
     return {"workload": "int4 g64 M=8 N=131072 K=2048 (134 MB weights), one launch",
-            "us_per_launch": dt * 1e6, "GB_s": b / dt / 1e9, "frac_hbm": b / dt / HBM_PEAK}
+            "us_per_launch": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "GB_s": b / dt / 1e9,
+            "frac_hbm": b / dt / HBM_PEAK}
 
 
 LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048),
@@ -245,32 +264,43 @@ def attainable(bits, M, N, K, group=64):
     return min(I8_PEAK, ai * HBM_PEAK)
 
 
+COLD = 320 * 1000 * 1000   # bytes of rotating weight copies: more than the 256 MB MALL
+
+
 def extra_cfg3(gpu):
-    ncp = 5                                         # 5 x 58 MB of int8 layers > MALL
+    """The seven M=256 int8 projections, each on weights rotating over more
+    than the MALL holds (a prefill reads its layer's weights from HBM), and
+    the layer as the forward pass issues it (four launches)."""
     res, tot_ops, tot_t = {}, 0.0, 0.0
     xs = {K: gpu.act(256, K) for K in (2048, 8192)}
     for K, (x, qs, pa) in xs.items():
         gpu.prep(x, qs, pa, 256, K)
     for name, N, K in LAYER:
+        ncp = -(-COLD // (N * K))
         ws = [gpu.w8(N, K) for _ in range(ncp)]
         x, qs, pa = xs[K]
         c = gpu.t.empty(256, N, device=gpu.dev)
-        dt = kernel_avg(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[i % ncp][0], ws[i % ncp][1], c), 20)
+        dt, lo, hi = kernel_time(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[i % ncp][0], ws[i % ncp][1], c),
+                                 max(20, ncp))
         ops = 2.0 * 256 * N * K
-        res[name] = {"us": dt * 1e6, "TOPS": ops / dt / 1e12, "frac_mfma": ops / dt / I8_PEAK,
-                     "frac_attainable": ops / dt / attainable(8, 256, N, K)}
+        res[name] = {"us": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "TOPS": ops / dt / 1e12,
+                     "frac_mfma": ops / dt / I8_PEAK, "frac_attainable": ops / dt / attainable(8, 256, N, K),
+                     "weight_copies": ncp}
         tot_ops += ops
         tot_t += dt
         del ws
+        gpu.t.cuda.empty_cache()
     # the layer as the forward pass issues it: q/k/v on one activation in one
-    # launch, o, gate/up in one launch, down (forward.rs:484-641)
-    lw = [{name: gpu.w8(N, K) for name, N, K in LAYER} for _ in range(3)]
+    # launch, o, gate/up in one launch, down (forward.rs:484-641); six copies
+    # of the layer's 58 MB
+    nl = 6
+    lw = [{name: gpu.w8(N, K) for name, N, K in LAYER} for _ in range(nl)]
     outs = {name: gpu.t.empty(256, N, device=gpu.dev) for name, N, K in LAYER}
 
     def item(i, name):
         N, K = next((N, K) for nm, N, K in LAYER if nm == name)
         x, qs, pa = xs[K]
-        w = lw[i % 3][name]
+        w = lw[i % nl][name]
         return (8, 256, N, K, pa, qs, w[0], w[1], outs[name])
 
     def layer(i):
@@ -280,12 +310,13 @@ def extra_cfg3(gpu):
         gpu.gemm_many([item(i, "down")])
     gs = gpu.graphs(layer, 12, 12)
     gpu.time_graphs(gs, 2)
-    lt = gpu.time_graphs(gs, 5) / (5 * 12)
-    return {"workload": "int8 prefill M=256, 7 projection shapes of one layer",
+    lt, llo, lhi = (x / 12 for x in med_range(gpu.time_each(gs, 7)))
+    return {"workload": "int8 prefill M=256, 7 projection shapes of one layer, weights rotating over "
+                        "> 256 MB (from HBM)",
             "per_shape": res, "layer_us": tot_t * 1e6, "TOPS": tot_ops / tot_t / 1e12,
             "frac_mfma": tot_ops / tot_t / I8_PEAK,
-            "layer_batched": {"launches": 4, "us": lt * 1e6, "TOPS": tot_ops / lt / 1e12,
-                              "frac_mfma": tot_ops / lt / I8_PEAK,
+            "layer_batched": {"launches": 4, "us": lt * 1e6, "us_range": [llo * 1e6, lhi * 1e6],
+                              "TOPS": tot_ops / lt / 1e12, "frac_mfma": tot_ops / lt / I8_PEAK,
                               "note": "q/k/v and gate/up each share one launch"},
             "tokens_per_s_30_layers": 256 / (30 * lt)}
 
@@ -328,8 +359,7 @@ def extra_cfg4(gpu):
 
     gs = gpu.graphs(step, 1, 1)
     gpu.time_graphs(gs, 3)
-    reps = 20
-    dt = gpu.time_graphs(gs, reps) / reps
+    dt, lo, hi = med_range(gpu.time_each(gs, 20))
     wbytes = 0
     for name, N, K in LAYER:
         wbytes += (N * K + N * 4) if name == "down" else (N * K // 2 + (K // 64) * N * 2)
@@ -340,7 +370,8 @@ def extra_cfg4(gpu):
     allb = allb * 30 + gemm_bytes(8, 8, 262144, 2048) + 30 * (3 * prep_bytes(8, 2048) + prep_bytes(8, 8192)) + prep_bytes(8, 2048)
     return {"workload": "decode step M=8: 30 layers + int8 LM head, 242 launches (q/k/v and "
                         "gate/up batched), one graph",
-            "us_per_step": dt * 1e6, "weight_bytes": wbytes, "GB_s_weights": wbytes / dt / 1e9,
+            "us_per_step": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "weight_bytes": wbytes,
+            "GB_s_weights": wbytes / dt / 1e9,
             "GB_s_all": allb / dt / 1e9, "frac_hbm": allb / dt / HBM_PEAK,
             "tokens_per_s": 8 / dt}
 
@@ -358,9 +389,9 @@ def extra_cfg5(gpu):
             fn = lambda i: gpu.q4g(2048, N, K, pa2, qs2, ws[i % 2][0], ws[i % 2][1], c)
         else:
             fn = lambda i: gpu.q8c(2048, N, K, pa8, qs8, ws[i % 2][0], ws[i % 2][1], c)
-        dt = kernel_avg(gpu, fn, 8, 3)
+        dt, lo, hi = kernel_time(gpu, fn, 8, 5)
         ops = 2.0 * 2048 * N * K
-        res[name] = {"bits": bits, "us": dt * 1e6, "TOPS": ops / dt / 1e12,
+        res[name] = {"bits": bits, "us": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "TOPS": ops / dt / 1e12,
                      "frac_mfma": ops / dt / I8_PEAK,
                      "frac_attainable": ops / dt / attainable(bits, 2048, N, K)}
     return {"workload": "long prefill M=2048 (gate/up int4 g64, down int8)", "per_shape": res}
@@ -435,6 +466,53 @@ def extra_ceilings(gpu):
                                    "us": dt * 1e6}
     return {"workload": "ceiling probes (fgm_ceil.hip): launch floor, one-launch read floors, "
                         "copy, int8 MFMA rate", **res}
+
+
+def extra_sweep(gpu):
+    """Where the paths cross on this GPU (bench/kernels/gemm_bench.c:105-133
+    measures the same on the CPU): the cfg2 up shape (N=8192, K=2048) at
+    M = 8 .. 512, int8 per-channel and int4 with group 64 / 128 / 256 / 512,
+    weights rotating over more than the MALL.  Reports each point's time and
+    path, the row count where the library switches from the skinny to the
+    dense kernel, and per group size the smallest M from which int8 is at
+    least as fast as int4 (the FGM_WEIGHTS=auto:M threshold this GPU
+    suggests; forward.rs:26-89 ships auto:16 for the CPU)."""
+    from fastgemma_amd import kernels
+    N, K = 8192, 2048
+    Ms = (8, 16, 32, 48, 64, 65, 96, 128, 256, 512)
+    groups = (64, 128, 256, 512)
+    n8 = -(-COLD // (N * K))
+    n4 = -(-COLD // (N * K // 2))
+    w8 = [gpu.w8(N, K) for _ in range(n8)]
+    w4 = [gpu.t.randint(0, 256, (N * K // 2,), dtype=gpu.t.uint8, device=gpu.dev) for _ in range(n4)]
+    s4 = {g: [(gpu.t.rand((K // g) * N, device=gpu.dev) * 0.045 + 0.005).half().view(gpu.t.int16)
+              for _ in range(n4)] for g in groups}
+    pts = {}
+    for M in Ms:
+        x, qs, pa = gpu.act(M, K)
+        gpu.prep(x, qs, pa, M, K)
+        c = gpu.t.empty(M, N, device=gpu.dev)
+        row = {}
+        dt = kernel_time(gpu, lambda i: gpu.q8c(M, N, K, pa, qs, w8[i % n8][0], w8[i % n8][1], c),
+                         max(16, n8), 3)[0]
+        row["q8c"] = {"us": dt * 1e6, "path": kernels.gemm_path(8, M, K)}
+        for g in groups:
+            dt = kernel_time(gpu, lambda i: gpu.q4g(M, N, K, pa, qs, w4[i % n4], s4[g][i % n4], c, g),
+                             max(16, n4), 3)[0]
+            row[f"q4g{g}"] = {"us": dt * 1e6, "path": kernels.gemm_path(4, M, K, g)}
+        for v in row.values():
+            v["TOPS"] = 2.0 * M * N * K / (v["us"] * 1e-6) / 1e12
+        pts[M] = row
+    switch = {k: next((M for M in Ms if pts[M][k]["path"] == "dense"), None) for k in pts[Ms[0]]}
+    int8_from = {}
+    for g in groups:
+        key = f"q4g{g}"
+        int8_from[key] = next((M for M in Ms if all(pts[m]["q8c"]["us"] <= pts[m][key]["us"]
+                                                    for m in Ms if m >= M)), None)
+    return {"workload": "M sweep on N=8192 K=2048: q8c and q4g g64..512, cold weights",
+            "points": {str(M): {k: {"us": round(v["us"], 2), "TOPS": round(v["TOPS"], 1), "path": v["path"]}
+                                for k, v in r.items()} for M, r in pts.items()},
+            "dense_from_M": switch, "int8_not_slower_from_M": int8_from}
 
 
 def extra_vendor(gpu):
@@ -686,76 +764,234 @@ def extra_model(gpu):
 
 
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline(host, budget_s=10.0):
+def bench_siblings():
+    """PIDs of other bench.py processes (a Python interpreter running this
+    script), matched on the executable name and the script argument, not on
+    the whole command line (a shell that mentions bench.py is no sibling;
+    fgm-bench main.rs:20-43 does the same on /proc/<pid>/comm)."""
+    me, out = os.getpid(), []
+    try:
+        pids = [int(d) for d in os.listdir("/proc") if d.isdigit()]
+    except OSError:
+        return out
+    for pid in pids:
+        if pid == me:
+            continue
+        try:
+            comm = open(f"/proc/{pid}/comm").read().strip()
+            argv = open(f"/proc/{pid}/cmdline", "rb").read().split(b"\0")
+        except OSError:
+            continue
+        if comm.startswith("python") and any(x.endswith(b"bench.py") for x in argv[1:3]):
+            out.append(pid)
+    return out
+
+
+def load_check(nt):
+    """The reference's guard against timing on a loaded host (fgm-bench
+    main.rs:45-113): another bench running refuses the CPU leg (unless
+    FGM_IGNORE_LOAD is set); a one-minute load average above 0.35 x threads
+    is reported with the numbers (this host is shared, so it warns rather
+    than refuses)."""
+    sibs = bench_siblings()
+    try:
+        la = float(open("/proc/loadavg").read().split()[0])
+    except (OSError, ValueError, IndexError):
+        la = None
+    return {"siblings": sibs, "loadavg_1m": la, "loaded": la is not None and la > 0.35 * nt,
+            "refuse": bool(sibs) and not os.environ.get("FGM_IGNORE_LOAD")}
+
+
+class CpuPath:
+    """The reference's own fgm_prep_rows + fgm_gemm_q8c_vnni / _q4g_vnni
+    (oracle/_ref, compiled from the reference's C) or, where that is not
+    built, the oracle's restatement, driven by the reference's thread split
+    (oracle/cpu_pool.c: pool.rs:110-145 for GEMMs, 16-row blocks for prep)."""
+
+    def __init__(self):
+        import oracle
+        self.o = oracle
+        self.L = oracle.lib()
+        R = oracle.ref()
+        self.kind = "reference" if R is not None else "port"
+        self.amx = bool(R is not None and R.fgm_cpu_has_amx())
+        self.nt = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+        self.nt = max(1, min(self.nt, 64))
+        src = R if R is not None else None
+        self.fq4 = C.cast(src.fgm_gemm_q4g_vnni if src else self.L.orc_gemm_q4g, C.c_void_p).value
+        self.fq8 = C.cast(src.fgm_gemm_q8c_vnni if src else self.L.orc_gemm_q8c, C.c_void_p).value
+        self.fprep = C.cast(src.fgm_prep_rows if src else self.L.orc_prep_rows, C.c_void_p).value
+        self.t1 = __import__("numpy").empty(1, "float64")
+        self.L.orc_pool_start(self.nt)
+
+    def close(self):
+        self.L.orc_pool_stop()
+
+    def act(self, M, K, seed):
+        import numpy as np
+        x = self.o.gen_normal(seed, M * K).reshape(M, K)
+        return dict(x=x, M=M, K=K, rot=np.empty((M, K), np.float32), qa=np.empty((M, K), np.int8),
+                    qs=np.empty(M, np.float32), pa=np.empty((M + 15) // 16 * 16 * K, np.int8))
+
+    def prep(self, a):
+        P = self.o._ptr
+        self.L.orc_pool_prep(self.fprep, P(a["x"]), a["K"], P(a["rot"]), P(a["qa"]), P(a["qs"]), P(a["pa"]),
+                             a["M"], a["K"], 0, 1, P(self.t1))
+
+    def gemm(self, bits, a, N, w, s, c, group=64):
+        P = self.o._ptr
+        if bits == 8:
+            self.L.orc_pool_q8c(self.fq8, a["M"], N, a["K"], P(a["pa"]), P(a["qs"]), P(w), P(s), P(c), N, 1,
+                                P(self.t1))
+        else:
+            self.L.orc_pool_q4g(self.fq4, a["M"], N, a["K"], P(a["pa"]), P(a["qs"]), P(w), P(s), group, P(c),
+                                N, 1, P(self.t1))
+
+
+def time_cpu(fn, min_reps=10, min_s=0.3):
+    """fn timed after one warm-up call: at least min_reps calls and min_s
+    seconds; (median, min, max, reps) in seconds, as fgm-bench main.rs:190-199
+    reports them."""
+    fn()
+    ts, t_end = [], time.perf_counter() + min_s
+    while len(ts) < min_reps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    m, lo, hi = med_range(ts)
+    return m, lo, hi, len(ts)
+
+
+def _rec(t, work, unit):
+    """A CPU row: median / min / max in ms and the median's throughput in the
+    GPU row's unit (work = bytes for GB/s, ops for TOPS)."""
+    m, lo, hi, n = t
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {"median_ms": m * 1e3, "min_ms": lo * 1e3, "max_ms": hi * 1e3, "reps": n,
+            "value": work / m / scale, "unit": unit}
+
+
+def cpu_configs(cp):
+    """Every BASELINE config on the CPU path, GEMM-only and prep + GEMM
+    on host-generated operands of the GPU rows'
+    shapes; the units and algorithmic work are the GPU rows'."""
     import numpy as np
-    import oracle
-    L = oracle.lib()
-    R = oracle.ref()
-    nt = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    nt = max(1, min(nt, 64))
-    L.orc_pool_start(nt)
-    kind = "reference" if R is not None else "port"
-    if R is not None:
-        fq4 = C.cast(R.fgm_gemm_q4g_vnni, C.c_void_p).value
-        fprep = C.cast(R.fgm_prep_rows, C.c_void_p).value
-    else:
-        fq4 = C.cast(L.orc_gemm_q4g, C.c_void_p).value
-        fprep = C.cast(L.orc_prep_rows, C.c_void_p).value
-    P = oracle._ptr
+    rng = np.random.default_rng(99)
+
+    def w8(N, K):
+        return (np.frombuffer(rng.bytes(N * K), np.int8).copy(),
+                (rng.random(N, dtype=np.float32) * 0.009 + 0.001).astype(np.float32))
+
+    def w4(N, K):
+        return (np.frombuffer(rng.bytes(N * K // 2), np.uint8).copy(),
+                (rng.random((K // 64) * N, dtype=np.float32) * 0.045 + 0.005).astype(np.float16).view(np.uint16))
+
+    out = {}
+    # cfg1: int8 GEMV M=1
+    a = cp.act(1, 2048, 31)
+    W = w8(8192, 2048)
+    c = np.empty((1, 8192), np.float32)
+    b = gemm_bytes(8, 1, 8192, 2048)
+    out["cfg1"] = {"gemm": _rec(time_cpu(lambda: cp.gemm(8, a, 8192, *W, c)), b, "GB/s"),
+                   "prep_gemm": _rec(time_cpu(lambda: (cp.prep(a), cp.gemm(8, a, 8192, *W, c))),
+                                     b + prep_bytes(1, 2048), "GB/s")}
+    # cfg3: the seven M=256 int8 projections, and the layer
+    acts = {K: cp.act(256, K, 40 + K) for K in (2048, 8192)}
+    r3, lay_g, lay_pg = {}, [], []
+    ws = {name: w8(N, K) for name, N, K in LAYER}
+    cs = {name: np.empty((256, N), np.float32) for name, N, K in LAYER}
+    for name, N, K in LAYER:
+        ops = 2.0 * 256 * N * K
+        g = _rec(time_cpu(lambda: cp.gemm(8, acts[K], N, *ws[name], cs[name]), 5), ops, "TOPS")
+        pg = _rec(time_cpu(lambda: (cp.prep(acts[K]), cp.gemm(8, acts[K], N, *ws[name], cs[name])), 5), ops,
+                  "TOPS")
+        r3[name] = {"gemm": g, "prep_gemm": pg}
+
+    def layer(with_prep):
+        for name, N, K in LAYER:
+            if with_prep and name in ("q", "o", "gate", "down"):
+                cp.prep(acts[K])
+            cp.gemm(8, acts[K], N, *ws[name], cs[name])
+    lops = sum(2.0 * 256 * N * K for _, N, K in LAYER)
+    r3["layer"] = {"gemm": _rec(time_cpu(lambda: layer(False), 5), lops, "TOPS"),
+                   "prep_gemm": _rec(time_cpu(lambda: layer(True), 5), lops, "TOPS")}
+    out["cfg3"] = r3
+    del ws, cs
+    # cfg4: 30 layers (q,k,v,o,gate,up int4 g64, down int8) + int8 LM head,
+    # distinct buffers, M=8, the forward pass's GEMM sequence
+    layers = [{name: (w8(N, K) if name == "down" else w4(N, K)) for name, N, K in LAYER} for _ in range(30)]
+    head = w8(262144, 2048)
+    a2, a8 = cp.act(8, 2048, 51), cp.act(8, 8192, 52)
+    outs = {name: np.empty((8, N), np.float32) for name, N, K in LAYER}
+    logits = np.empty((8, 262144), np.float32)
+    shp = {name: (N, K) for name, N, K in LAYER}
+
+    def step(with_prep):
+        for L in layers:
+            for grp in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+                a = a8 if grp[0] == "down" else a2
+                if with_prep:
+                    cp.prep(a)
+                for name in grp:
+                    cp.gemm(8 if name == "down" else 4, a, shp[name][0], *L[name], outs[name])
+        if with_prep:
+            cp.prep(a2)
+        cp.gemm(8, a2, 262144, *head, logits)
+    allb = sum(gemm_bytes(8 if name == "down" else 4, 8, N, K) for name, N, K in LAYER) * 30 \
+        + gemm_bytes(8, 8, 262144, 2048)
+    preps = 30 * (3 * prep_bytes(8, 2048) + prep_bytes(8, 8192)) + prep_bytes(8, 2048)
+    out["cfg4"] = {"gemm": _rec(time_cpu(lambda: step(False), 5, 0.2), allb, "GB/s"),
+                   "prep_gemm": _rec(time_cpu(lambda: step(True), 5, 0.2), allb + preps, "GB/s")}
+    del layers, head
+    # cfg5: M=2048 heavy-tailed (gate/up int4 g64, down int8)
+    r5 = {}
+    x5 = {K: cp.act(2048, K, 60 + K) for K in (2048, 8192)}
+    for K, a in x5.items():
+        a["x"][:] = (cp.o.gen_student_t(61 + K, 2048 * K, 3)).reshape(2048, K)
+    for name, bits, N, K in (("gate", 4, 8192, 2048), ("up", 4, 8192, 2048), ("down", 8, 2048, 8192)):
+        W = w4(N, K) if bits == 4 else w8(N, K)
+        c = np.empty((2048, N), np.float32)
+        ops = 2.0 * 2048 * N * K
+        r5[name] = {"bits": bits,
+                    "gemm": _rec(time_cpu(lambda: cp.gemm(bits, x5[K], N, *W, c), 5, 0.2), ops, "TOPS"),
+                    "prep_gemm": _rec(time_cpu(lambda: (cp.prep(x5[K]), cp.gemm(bits, x5[K], N, *W, c)), 5, 0.2),
+                                      ops, "TOPS")}
+    out["cfg5"] = r5
+    return out
+
+
+def cpu_baseline(host, budget_s=10.0):
+    """The headline's CPU leg (cfg2: prep + q4g up, prep + q4g down, M=8) for
+    about budget_s seconds, and every other config (cpu_configs)."""
+    import numpy as np
+    cp = CpuPath()
+    chk = load_check(cp.nt)
+    if chk["refuse"]:
+        cp.close()
+        return {"refused": f"other bench.py processes running: {chk['siblings']} (set FGM_IGNORE_LOAD=1 "
+                           "to time anyway)", "load": chk}
+    P = cp.o._ptr
     shapes = (("up", 8192, 2048), ("down", 2048, 8192))
     bufs = {}
     for name, N, K in shapes:
         w, s = host[name]
-        x = oracle.gen_normal(5, 8 * K).reshape(8, K)
-        bufs[name] = dict(w=np.ascontiguousarray(w), s=np.ascontiguousarray(s), x=x,
-                          rot=np.empty((8, K), np.float32), qa=np.empty((8, K), np.int8),
-                          qs=np.empty(8, np.float32), pa=np.empty(16 * K, np.int8),
-                          c=np.empty((8, N), np.float32), N=N, K=K)
-    t1 = np.empty(1, np.float64)
+        bufs[name] = dict(a=cp.act(8, K, 5), w=np.ascontiguousarray(w), s=np.ascontiguousarray(s),
+                          c=np.empty((8, N), np.float32), N=N)
 
-    def one_step():
+    def one_step(with_prep=True):
         for name, N, K in shapes:
             b = bufs[name]
-            L.orc_pool_prep(fprep, P(b["x"]), K, P(b["rot"]), P(b["qa"]), P(b["qs"]), P(b["pa"]),
-                            8, K, 0, 1, P(t1))
-            L.orc_pool_q4g(fq4, 8, N, K, P(b["pa"]), P(b["qs"]), P(b["w"]), P(b["s"]), 64,
-                           P(b["c"]), N, 1, P(t1))
+            if with_prep:
+                cp.prep(b["a"])
+            cp.gemm(4, b["a"], N, b["w"], b["s"], b["c"])
 
-    one_step()  # warm-up pass over the weights
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 10:
-        t0 = time.perf_counter()
-        one_step()
-        times.append(time.perf_counter() - t0)
-
-    # the prefill row beside it: BASELINE configs[2]'s q projection (M=256,
-    # N=2048, K=2048, int8 per-channel) through the reference's
-    # fgm_gemm_q8c_vnni with the same N-split, for about a quarter of the budget
-    fq8 = C.cast(R.fgm_gemm_q8c_vnni if R is not None else L.orc_gemm_q8c, C.c_void_p).value
-    Mp, Np, Kp = 256, 2048, 2048
-    ap = oracle.gen_i8(21, Mp * Kp, -127, 127)
-    pa8 = oracle.pack_a(Mp, Kp, ap.reshape(Mp, Kp))
-    as8 = oracle.gen_uniform(22, Mp, 1e-3, 1e-2)
-    w8 = oracle.gen_i8(23, Np * Kp, -127, 127)
-    s8 = oracle.gen_uniform(24, Np, 1e-3, 1e-2)
-    c8 = np.empty((Mp, Np), np.float32)
-
-    def one_gemm():
-        L.orc_pool_q8c(fq8, Mp, Np, Kp, P(pa8), P(as8), P(w8), P(s8), P(c8), Np, 1, P(t1))
-
-    one_gemm()
-    ptimes = []
-    t_end = time.perf_counter() + budget_s / 4
-    while time.perf_counter() < t_end or len(ptimes) < 5:
-        t0 = time.perf_counter()
-        one_gemm()
-        ptimes.append(time.perf_counter() - t0)
-    L.orc_pool_stop()
-    pmed = sorted(ptimes)[len(ptimes) // 2]
-    med = sorted(times)[len(times) // 2]
     step_bytes = (gemm_bytes(4, 8, 8192, 2048) + gemm_bytes(4, 8, 2048, 8192)
                   + prep_bytes(8, 2048) + prep_bytes(8, 8192))
+    t = time_cpu(one_step, 10, budget_s)
+    tg = time_cpu(lambda: one_step(False), 10, budget_s / 4)
+    per = cpu_configs(cp)
+    cp.close()
+    after = bench_siblings()
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -764,19 +1000,16 @@ def cpu_baseline(host, budget_s=10.0):
                 break
     except OSError:
         pass
-    amx = bool(R is not None and R.fgm_cpu_has_amx())
     phys, smt = cpu_topology()
-    return {"value": step_bytes / med / 1e9, "unit": "GB/s", "cores": nt, "kind": kind,
-            "physical_cores": phys, "smt_used": smt,
-            "sample": f"{len(times)} steps of cfg2 (prep + q4g up + prep + q4g down, M=8) in "
-                      f"~{budget_s:.0f} s, median step {med * 1e3:.3f} ms; reference "
-                      f"fgm_prep_rows + fgm_gemm_q4g_vnni, pool.rs N-split over {nt} threads "
-                      f"({phys} physical cores, SMT {'used' if smt else 'not used'}); "
-                      f"host '{cpu}', AMX present: {amx} (AMX path not timed)",
-            "prefill": {"value": 2.0 * Mp * Np * Kp / pmed / 1e12, "unit": "TOPS",
-                        "sample": f"{len(ptimes)} runs of fgm_gemm_q8c_vnni M={Mp} N={Np} K={Kp} "
-                                  f"(BASELINE configs[2] q) on the same {nt} threads, median "
-                                  f"{pmed * 1e3:.3f} ms"}}
+    gemm_b = gemm_bytes(4, 8, 8192, 2048) + gemm_bytes(4, 8, 2048, 8192)
+    return {"value": step_bytes / t[0] / 1e9, "unit": "GB/s", "cores": cp.nt, "kind": cp.kind,
+            "physical_cores": phys, "smt_used": smt, "amx": cp.amx,
+            "sample": f"{t[3]} cfg2 steps (prep+q4g up, prep+q4g down, M=8) in ~{budget_s:.0f} s: median "
+                      f"{t[0] * 1e3:.3f} ms, range {t[1] * 1e3:.3f}-{t[2] * 1e3:.3f} ms; {cp.kind} VNNI kernels, "
+                      f"pool.rs N-split over {cp.nt} threads ({phys} cores); '{cpu}'",
+            "cfg2": {"prep_gemm": _rec(t, step_bytes, "GB/s"), "gemm": _rec(tg, gemm_b, "GB/s")},
+            "per_config": per,
+            "load": {**chk, "siblings_after": after, "suspect": bool(after) or chk["loaded"]}}
 
 
 def cpu_topology():
@@ -807,17 +1040,83 @@ def read_traffic():
     return None
 
 
+def host_cfg2_weights():
+    """cfg2's up / down int4 weights generated on the host (for --only cpu)."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    out = {}
+    for name, N, K in (("up", 8192, 2048), ("down", 2048, 8192)):
+        out[name] = (np.frombuffer(rng.bytes(N * K // 2), np.uint8).copy(),
+                     (rng.random((K // 64) * N, dtype=np.float32) * 0.045 + 0.005).astype(np.float16).view(np.uint16))
+    return out
+
+
+def _r(x, nd=3):
+    """x to nd significant digits (compact summary)."""
+    if x is None:
+        return None
+    if isinstance(x, (list, tuple)):
+        return [_r(v, nd) for v in x]
+    return float(f"{x:.{nd}g}")
+
+
+def summary(out):
+    """The figures a reader needs, compact, printed last in the JSON line:
+    GPU time (median, and range where measured), the roofline fraction, and
+    the CPU row beside it (GPU / CPU speed-up on the same algorithmic work)."""
+    ex, cpu = out.get("extra", {}), out.get("cpu_baseline") or {}
+    per = cpu.get("per_config", {})
+    sm = {"cfg2_step_us": _r(out["ms_per_step"] * 1e3), "cfg2_step_range_us": _r(out.get("step_range_us")),
+          "cfg2_frac_hbm": _r(out["config"]["frac_hbm_step"]),
+          "pair_launch_us": _r(out["roofline"]["us_per_launch"]), "pair_frac_hbm": _r(out["roofline"]["frac"])}
+    if cpu.get("cfg2"):
+        sm["cfg2_cpu_ms"] = _r(cpu["cfg2"]["prep_gemm"]["median_ms"])
+    c1 = ex.get("cfg1", {})
+    if "us_per_launch" in c1:
+        sm["cfg1"] = {"us": _r(c1["us_per_launch"]), "frac_hbm": _r(c1["frac_hbm"])}
+        if "cfg1" in per:
+            sm["cfg1"]["cpu_ms"] = _r(per["cfg1"]["gemm"]["median_ms"])
+    s4 = ex.get("int4_stream", {})
+    if "us_per_launch" in s4:
+        sm["int4_134MB"] = {"us": _r(s4["us_per_launch"]), "frac_hbm": _r(s4["frac_hbm"])}
+    c3 = ex.get("cfg3", {})
+    if "per_shape" in c3:
+        sm["cfg3_us"] = {k: _r(v["us"]) for k, v in c3["per_shape"].items()}
+        lb = c3["layer_batched"]
+        sm["cfg3_layer"] = {"us": _r(lb["us"]), "range": _r(lb.get("us_range")), "frac_mfma": _r(lb["frac_mfma"])}
+        if "cfg3" in per:
+            sm["cfg3_layer"]["cpu_ms"] = _r(per["cfg3"]["layer"]["gemm"]["median_ms"])
+    c4 = ex.get("cfg4", {})
+    if "us_per_step" in c4:
+        sm["cfg4"] = {"us": _r(c4["us_per_step"]), "frac_hbm": _r(c4["frac_hbm"]), "tok_s": _r(c4["tokens_per_s"])}
+        if "cfg4" in per:
+            sm["cfg4"]["cpu_ms"] = _r(per["cfg4"]["prep_gemm"]["median_ms"])
+    c5 = ex.get("cfg5", {})
+    if "per_shape" in c5:
+        sm["cfg5"] = {k: {"us": _r(v["us"]), "frac_mfma": _r(v["frac_mfma"])} for k, v in c5["per_shape"].items()}
+        for k in sm["cfg5"]:
+            if k in per.get("cfg5", {}):
+                sm["cfg5"][k]["cpu_ms"] = _r(per["cfg5"][k]["gemm"]["median_ms"])
+    sw = ex.get("sweep", {})
+    if "dense_from_M" in sw:
+        sm["sweep"] = {"dense_from_M": sw["dense_from_M"].get("q8c"), "int8_not_slower_from_M": sw["int8_not_slower_from_M"]}
+    if cpu:
+        sm["cpu"] = {"kind": cpu.get("kind"), "cores": cpu.get("cores"), "suspect": cpu.get("load", {}).get("suspect")}
+    return sm
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--reps", type=int, default=7, help="timed replays of the K-step graph (median reported)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
-                    help="run one extra measurement (ceilings, cfg1, int4_stream, cfg3, vendor, cfg5, cfg4, elem, "
-                         "prep_fused, attn, model) and print its JSON instead of the headline line")
+                    help="run one extra measurement (ceilings, cfg1, int4_stream, cfg3, vendor, sweep, cfg5, cfg4, "
+                         "elem, prep_fused, attn, model, cpu) and print its JSON instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -825,18 +1124,21 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.only == "cpu":
+        print(json.dumps({"cpu": cpu_baseline(host_cfg2_weights(), args.cpu_seconds)}))
+        return
     gpu = Gpu()
     gpu.t.manual_seed(1234)
     # the ceilings go last: their large rotating buffers must not disturb the
     # other measurements' allocations
     extras = {"cfg1": extra_cfg1, "int4_stream": extra_int4_stream,
-              "cfg3": extra_cfg3, "vendor": extra_vendor,
+              "cfg3": extra_cfg3, "vendor": extra_vendor, "sweep": extra_sweep,
               "cfg5": extra_cfg5, "cfg4": extra_cfg4, "elem": extra_elem,
               "prep_fused": extra_prep_fused, "attn": extra_attn,
               "model": extra_model, "ceilings": extra_ceilings}
     if args.only is not None:
         if args.only not in extras:
-            print(f"--only: unknown measurement {args.only!r} (one of {', '.join(extras)})",
+            print(f"--only: unknown measurement {args.only!r} (one of {', '.join(extras)}, cpu)",
                   file=sys.stderr)
             sys.exit(2)
         print(json.dumps({args.only: extras[args.only](gpu)}))
@@ -844,18 +1146,19 @@ def main():
     log("setting up cfg2 (48 weight copies)")
     step, gemv_pair, gemv_up, gemv_down, step_bytes, host = cfg2_setup(gpu)
 
-    chunk = 16
-    warm = gpu.graphs(step, max(chunk, args.warmup), chunk)
+    warm = gpu.graphs(step, max(16, args.warmup), 16)
     gpu.time_graphs(warm)
-    # exactly `steps` steps: full chunks plus one remainder graph
-    gs = gpu.graphs(step, args.steps, chunk)
-    log(f"timing {args.steps} steps in {len(gs)} graphs")
-    dt = gpu.time_graphs(gs)
+    # all `steps` steps in one graph; each timed replay is exactly `steps`
+    # steps, synchronized on both sides; the median replay is reported
+    gs = gpu.graphs(step, args.steps, args.steps)
+    log(f"timing {args.steps} steps in one graph, {args.reps} replays")
+    dt, dlo, dhi = med_range(gpu.time_each(gs, max(5, args.reps)))
     ms_per_step = dt / args.steps * 1e3
     value = step_bytes * args.steps / dt / 1e9
+    del gs, warm
 
     log("dominant kernel timing")
-    pair_s = kernel_avg(gpu, gemv_pair)
+    pair_s, pair_lo, pair_hi = kernel_time(gpu, gemv_pair)
     up_s = kernel_avg(gpu, gemv_up)
     down_s = kernel_avg(gpu, gemv_down)
     up_b = gemm_bytes(4, 8, 8192, 2048)
@@ -866,7 +1169,8 @@ def main():
             "kernel": "decode_kernel (int4, M <= 8 variant): the step's GEMM launch, "
                       "up N=8192 K=2048 and down N=2048 K=8192 in one launch, M=8",
             "algorithmic_bytes_per_launch": pair_b, "us_per_launch": pair_s * 1e6,
-            "timing": "HIP events around a graph of 48 back-to-back launches / 48",
+            "us_range": [pair_lo * 1e6, pair_hi * 1e6],
+            "timing": "HIP events around a graph of 48 back-to-back launches / 48, median of 5 replays",
             "single_shape_launches": {
                 "up": {"us": up_s * 1e6, "GB_s": up_b / up_s / 1e9, "frac": up_b / up_s / HBM_PEAK},
                 "down": {"us": down_s * 1e6, "GB_s": down_b / down_s / 1e9,
@@ -901,10 +1205,14 @@ def main():
                                "up N=8192 K=2048 + down N=2048 K=8192",
                    "global_batch": 8, "algorithmic_bytes_per_step": step_bytes,
                    "frac_hbm_step": value * 1e9 / HBM_PEAK},
+        "timing": f"one graph of {args.steps} steps, median of {max(5, args.reps)} timed replays",
+        "step_range_us": [dlo / args.steps * 1e6, dhi / args.steps * 1e6],
         "roofline": roof,
         "cpu_baseline": cpu,
         "extra": extra,
     }
+    out["summary"] = summary(out)
+    log("done")
     print(json.dumps(out))
 
 

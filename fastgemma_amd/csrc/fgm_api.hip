@@ -113,9 +113,17 @@ int check_gemm(int m, int n, int k, int ldc, int n0, int n1, int bits, int group
   return check_ranges(bits, m, n, k, group);
 }
 
-// Skinny kernel for m <= 64 when its LDS fits, else the dense MFMA kernel.
+// The skinny weight-stream kernel up to the row count where the dense MFMA
+// kernel overtakes it, when its LDS fits; else the dense kernel.  Crossovers
+// measured on MI355X (bench.py --only sweep, N = 8192, K = 2048, cold
+// weights; skinny / dense us): int8 M = 32: 7.3 / 7.7, M = 48: 8.6 / 8.0;
+// int4 group 64 M = 48: 12.2 / 12.7, M = 64: 18.3 / 12.8; int4 wider groups
+// (the skinny kernel's general-group chain) M = 16: 8.4 / 13.1, M = 32:
+// 17.5 / 12.5.
+int skinny_max_rows(int bits, int group) { return bits == 8 ? 32 : (group == 64 ? 48 : 16); }
+
 int gemm_path(int bits, int m, int k, int group) {
-  return fgm_decode_fits(bits, m, k, group) ? 0 : 1;
+  return (m <= skinny_max_rows(bits, group) && fgm_decode_fits(bits, m, k, group)) ? 0 : 1;
 }
 
 GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, const void* b,

@@ -122,9 +122,17 @@ def test_no_gpu_means_no_backend():
 
 
 def test_skinny_dense_dispatch_thresholds():
+    """The switch points measured on MI355X (bench.py --only sweep): the
+    skinny kernel up to 32 rows for int8, 48 for int4 group 64, 16 for wider
+    int4 groups; the dense kernel beyond."""
     assert K.gemm_path(8, 1, 2048) == "skinny"
     assert K.gemm_path(4, 8, 8192, 64) == "skinny"
-    assert K.gemm_path(8, 64, 2048) == "skinny"
+    assert K.gemm_path(8, 32, 2048) == "skinny"
+    assert K.gemm_path(8, 33, 2048) == "dense"
+    assert K.gemm_path(4, 48, 2048, 64) == "skinny"
+    assert K.gemm_path(4, 49, 2048, 64) == "dense"
+    assert K.gemm_path(4, 16, 2048, 128) == "skinny"
+    assert K.gemm_path(4, 17, 2048, 256) == "dense"
     assert K.gemm_path(8, 65, 2048) == "dense"
     assert K.gemm_path(4, 256, 2048, 64) == "dense"
     # the int4 skinny kernel keeps every group's sums in LDS; past 160 KB it goes dense
