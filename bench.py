@@ -456,6 +456,7 @@ def extra_ceilings(gpu):
                           "GB_s": 2 * nbytes / dt / 1e9}
     del src, dst
     t.cuda.empty_cache()
+    res["grid_barrier"] = ceil_gridbar(gpu, L, ok)
     iters = 2000
     for shape, ops1 in ((32, 65536), (16, 32768)):
         nwg = 1024
@@ -513,6 +514,44 @@ def extra_sweep(gpu):
             "points": {str(M): {k: {"us": round(v["us"], 2), "TOPS": round(v["TOPS"], 1), "path": v["path"]}
                                 for k, v in r.items()} for M, r in pts.items()},
             "dense_from_M": switch, "int8_not_slower_from_M": int8_from}
+
+
+def ceil_gridbar(gpu, L, ok):
+    """Cost of one device-wide barrier inside a cooperative launch (what a
+    persistent kernel spanning a layer's dependent GEMMs would pay instead of
+    a kernel boundary, ~1.66 us here): per variant (fgm_ceil.hip) and grid,
+    (time of 250 barriers - time of 50) / 200, every workgroup handing 2 KB
+    across each barrier; stale reads and spin-limit exits are counted."""
+    import ctypes as C
+    L.fgm_ceil_gridbar.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.fgm_ceil_gridbar_bytes.restype = C.c_size_t
+    t = gpu.t
+    names = {0: "agent fences, acquire polls", 1: "agent fences, relaxed polls",
+             2: "agent fences, relaxed polls, non-temporal outputs", 3: "no fences (atomics only)",
+             4: "8 group counters, one release fence per group, relaxed polls",
+             5: "8 group counters, no fences (atomics only)"}
+    out = {}
+    for v in (0, 1, 2, 3, 4, 5):
+        for nwg in (256, 512):
+            bar = t.zeros(L.fgm_ceil_gridbar_bytes() // 4, dtype=t.int32, device=gpu.dev)
+            buf = t.zeros(2 * nwg * 512, dtype=t.float32, device=gpu.dev)
+            stale = t.zeros(1, dtype=t.int32, device=gpu.dev)
+
+            def run(iters):
+                bar.zero_()
+                e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                e0.record()
+                ok(L.fgm_ceil_gridbar(v, nwg, iters, bar.data_ptr(), buf.data_ptr(), stale.data_ptr(),
+                                      gpu.stream()))
+                e1.record()
+                t.cuda.synchronize()
+                return e0.elapsed_time(e1) / 1e3, int(bar[2].item())
+            run(50)
+            t_lo, e_lo = run(50)
+            t_hi, e_hi = run(250)
+            out[f"v{v} {nwg}wg"] = {"variant": names[v], "us_per_barrier": (t_hi - t_lo) / 200 * 1e6,
+                                    "stale_reads": int(stale.item()), "spin_limit_hit": bool(e_lo or e_hi)}
+    return out
 
 
 def extra_vendor(gpu):

@@ -13,6 +13,10 @@
 //                   traffic figures (its algorithmic bytes are known exactly)
 //   fgm_ceil_mfma   independent int8 MFMA chains on every SIMD: the dense int8
 //                   peak (v_mfma_i32_32x32x32_i8 or v_mfma_i32_16x16x64_i8)
+//   fgm_ceil_gridbar  a device-wide barrier between dependent steps inside one
+//                   cooperative launch (what a persistent decode kernel would
+//                   pay per dependent GEMM instead of a kernel boundary), with
+//                   the 2 KB per workgroup a decode GEMM hands on
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -111,6 +115,110 @@ __global__ __launch_bounds__(256) void mfma_kernel(int iters, int* sink) {
   }
 }
 
+// Device-wide barrier variants (one wave per workgroup arrives; the others
+// wait at the workgroup barrier).  Each iteration every workgroup writes 2 KB
+// (512 floats, as a decode GEMM's 8 x 64 output slice), crosses the barrier
+// and reads the 2 KB another workgroup wrote, counting stale values.
+//   0: agent-scope release fence, acq_rel arrival, every poll an agent-scope
+//      acquire load
+//   1: agent-scope release fence, relaxed arrival, relaxed polls, one
+//      agent-scope acquire fence after the poll
+//   2: as 1, the 2 KB stored non-temporally (streamed past the L2)
+//   3: relaxed arrival and polls, no fences (the atomic round trip alone;
+//      the data may be stale, which the count shows)
+//   4: hierarchical: workgroup b arrives at group counter b % 8 (the XCD it
+//      is dispatched to when workgroups go round-robin over the eight XCDs),
+//      the group's last arriver takes one agent-scope release fence for the
+//      group and arrives at the top counter; relaxed polls, one agent-scope
+//      acquire fence per workgroup after them
+//   5: as 4 without fences (the hierarchical atomics alone)
+// Spins are bounded: past the limit the workgroup raises bar[2] and every
+// later barrier is skipped, so the grid always drains.
+struct GridBar {
+  uint32_t count, gen, err, pad[29];
+  uint32_t grp[8][32];  // variants 4-5: group counters, one 128-byte line each
+};
+
+template <int V>
+FGM_DEV void grid_barrier(GridBar* b, uint32_t nwg, uint32_t spin_limit) {
+  if constexpr (V >= 4) {
+    __syncthreads();
+    if (threadIdx.x == 0 && !__hip_atomic_load(&b->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      const uint32_t grp = blockIdx.x & 7, ngrp = nwg < 8 ? nwg : 8;
+      const uint32_t members = nwg / 8 + (grp < nwg % 8 ? 1u : 0u);
+      const uint32_t g = __hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t a = __hip_atomic_fetch_add(&b->grp[grp][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bool last = false;
+      if (a == members - 1) {
+        __hip_atomic_store(&b->grp[grp][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (V == 4) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        last = __hip_atomic_fetch_add(&b->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ngrp - 1;
+      }
+      if (last) {
+        __hip_atomic_store(&b->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&b->gen, g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        uint32_t spins = 0;
+        while (__hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g) {
+          if (++spins > spin_limit) {
+            __hip_atomic_store(&b->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+        }
+      }
+      if (V == 4) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    return;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && !__hip_atomic_load(&b->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    if (V != 3) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t g = __hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t arrived = V == 0 ? __hip_atomic_fetch_add(&b->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT)
+                                    : __hip_atomic_fetch_add(&b->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (arrived == nwg - 1) {
+      __hip_atomic_store(&b->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&b->gen, g + 1, V == 0 ? __ATOMIC_RELEASE : __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      uint32_t spins = 0;
+      while ((V == 0 ? __hip_atomic_load(&b->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)
+                     : __hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == g) {
+        if (++spins > spin_limit) {
+          __hip_atomic_store(&b->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+    }
+    if (V == 1 || V == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+}
+
+template <int V>
+__global__ __launch_bounds__(256) void gridbar_kernel(GridBar* b, float* buf, int iters, uint32_t spin_limit,
+                                                      uint32_t* stale) {
+  const uint32_t nwg = gridDim.x, wg = blockIdx.x, t = threadIdx.x;
+  uint32_t bad = 0;
+  for (int i = 0; i < iters; i++) {
+    float* mine = buf + ((size_t)(i & 1) * nwg + wg) * 512;
+    const float v = (float)(i * 4096 + (int)wg);
+    if (V == 2) {
+      __builtin_nontemporal_store(v, mine + t);
+      __builtin_nontemporal_store(v, mine + 256 + t);
+    } else {
+      mine[t] = v;
+      mine[256 + t] = v;
+    }
+    grid_barrier<V>(b, nwg, spin_limit);
+    const uint32_t o = (wg + 1) % nwg;
+    const float* other = buf + ((size_t)(i & 1) * nwg + o) * 512;
+    const float want = (float)(i * 4096 + (int)o);
+    bad += (other[t] != want) + (other[256 + t] != want);
+  }
+  if (bad) atomicAdd(stale, bad);
+}
+
 }  // namespace
 
 extern "C" {
@@ -180,6 +288,28 @@ int fgm_ceil_mfma(int shape, int nwg, int iters, int* sink, void* stream) {
   else
     hipLaunchKernelGGL(mfma_kernel<false>, dim3(nwg), dim3(256), 0, (hipStream_t)stream, iters, sink);
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Cooperative launch of nwg workgroups (256 threads) running `iters`
+// barriers of variant v (0 .. 5).  bar: fgm_ceil_gridbar_bytes() bytes, zeroed
+// by the caller before each launch (word 2 is set when a spin limit was hit);
+// buf: 2 x nwg x 512 floats; stale: one word (stale reads are added).
+// Returns 0, 1 for bad arguments, 2 for a failed launch.
+size_t fgm_ceil_gridbar_bytes(void) { return sizeof(GridBar); }
+
+int fgm_ceil_gridbar(int v, int nwg, int iters, void* bar, float* buf, uint32_t* stale, void* stream) {
+  if (v < 0 || v > 5 || nwg < 1 || iters < 1 || !bar || !buf || !stale) return 1;
+  const uint32_t spin_limit = 1u << 20;
+  GridBar* b = (GridBar*)bar;
+  void* args[] = {&b, &buf, &iters, (void*)&spin_limit, &stale};
+  const void* k = v == 0 ? (const void*)gridbar_kernel<0>
+                : v == 1 ? (const void*)gridbar_kernel<1>
+                : v == 2 ? (const void*)gridbar_kernel<2>
+                : v == 3 ? (const void*)gridbar_kernel<3>
+                : v == 4 ? (const void*)gridbar_kernel<4>
+                         : (const void*)gridbar_kernel<5>;
+  hipError_t e = hipLaunchCooperativeKernel(k, dim3(nwg), dim3(256), args, 0, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : 2;
 }
 
 }  // extern "C"
