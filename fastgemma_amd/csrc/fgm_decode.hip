@@ -122,22 +122,24 @@ __host__ __device__ inline int pitch4(int n) {
   return ((r4 / 4) & 1) ? r4 : r4 + 4;
 }
 
-// Ring slots per stream wave.
-#ifndef FGM_DEC_D
-#define FGM_DEC_D 5               // ring slots per stream wave (M <= 8)
-#endif
-__host__ __device__ constexpr int ring_depth(int bits, int MB, bool half) {
-  return half ? FGM_DEC_D : (bits == 8 ? 4 : (MB == 1 ? 4 : (MB == 2 ? 3 : 2)));
+// Ring slots per stream wave.  M <= 8: fewer units in flight per wave suit
+// the grids of one round of workgroups (measured with 2-5 slots, ~4 units per
+// wave: the cfg2 pair 7.9 -> 7.7 us with 4 slots, the int8 M = 1 GEMV 5.45 ->
+// 5.26 us with 3); the park in the ring needs a slot for every unit of a
+// wave, so it keeps 5.
+__host__ __device__ constexpr int ring_depth(int bits, int MB, bool half, bool pir = false) {
+  return half ? (pir ? 5 : (bits == 8 ? 3 : 4))
+              : (bits == 8 ? 4 : (MB == 1 ? 4 : (MB == 2 ? 3 : 2)));
 }
 
 // Shape constants of a kernel variant.
-template <int BITS, int MB, bool HALF>
+template <int BITS, int MB, bool HALF, bool PIR = false>
 struct Geo {
   static constexpr int TPU = BITS == 4 ? 2 : 1;       // k-tiles per 1 KB unit
   static constexpr int OUT = HALF ? 128 : 256 * MB;   // outputs per n-block
   static constexpr int NA = HALF ? 1 : MB * TPU;      // activation loads per unit
   static constexpr int X = 1 + NA;                    // vector-memory instructions per unit
-  static constexpr int D = ring_depth(BITS, MB, HALF);
+  static constexpr int D = ring_depth(BITS, MB, HALF, PIR);
 };
 
 // LDS layout of one workgroup (bytes), shared by the host (sizing) and the
@@ -184,7 +186,7 @@ struct Lay {
 // (int4, M <= 8, group 64, every slot filled once: UPW <= D).
 template <int BITS, int MB, bool HALF, bool G1, bool RAW, bool PIR = false>
 __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
-  using G = Geo<BITS, MB, HALF>;
+  using G = Geo<BITS, MB, HALF, PIR>;
   static_assert(!PIR || (BITS == 4 && HALF && G1 && !RAW), "park in ring: int4, M <= 8, group 64");
   constexpr int TPU = G::TPU, OUT = G::OUT, NA = G::NA, X = G::X, D = G::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -546,7 +548,7 @@ Lay lay_for(int bits, int M, int K, int ks, int nws, int nbw, bool pir = false) 
   const int out = half ? 128 : 256 * MB;
   const int tpu = bits == 4 ? 2 : 1;
   const int upw = ((K / 64 + tpu - 1) / tpu + ks - 1) / ks;
-  return Lay(bits, out, ring_depth(bits, MB, half), ks, upw, nws, nbw, K / 64, half ? 8 : 16 * MB, pir);
+  return Lay(bits, out, ring_depth(bits, MB, half, pir), ks, upw, nws, nbw, K / 64, half ? 8 : 16 * MB, pir);
 }
 
 // Does one problem fit a workgroup of nws waves with nbw n-blocks?
@@ -663,7 +665,7 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   long nwg_plain = 0;
   for (int i = 0; i < bt.count; i++) {
     const GemmProb& p = bt.p[i];
-    pir = pir && p.tw <= ring_depth(4, 1, true);
+    pir = pir && p.tw <= ring_depth(4, 1, true, true);
     nwg_plain += (p.nblocks + NWS / p.ks - 1) / (NWS / p.ks);
   }
   pir = pir && nwg_plain > FGM_DEC_PIR_MIN_WGS;
