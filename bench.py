@@ -282,10 +282,12 @@ def extra_cfg3(gpu):
         c = gpu.t.empty(256, N, device=gpu.dev)
         dt, lo, hi = kernel_time(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[i % ncp][0], ws[i % ncp][1], c),
                                  max(20, ncp))
+        # the same launch on one weight copy (L2 / MALL resident), for reference
+        wt = kernel_time(gpu, lambda i: gpu.q8c(256, N, K, pa, qs, ws[0][0], ws[0][1], c), 20)[0]
         ops = 2.0 * 256 * N * K
         res[name] = {"us": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "TOPS": ops / dt / 1e12,
                      "frac_mfma": ops / dt / I8_PEAK, "frac_attainable": ops / dt / attainable(8, 256, N, K),
-                     "weight_copies": ncp}
+                     "weight_copies": ncp, "us_one_copy": wt * 1e6}
         tot_ops += ops
         tot_t += dt
         del ws
@@ -311,13 +313,17 @@ def extra_cfg3(gpu):
     gs = gpu.graphs(layer, 12, 12)
     gpu.time_graphs(gs, 2)
     lt, llo, lhi = (x / 12 for x in med_range(gpu.time_each(gs, 7)))
+    g1 = gpu.graphs(lambda i: layer(0), 12, 12)
+    gpu.time_graphs(g1, 2)
+    l1 = med_range(gpu.time_each(g1, 7))[0] / 12
     return {"workload": "int8 prefill M=256, 7 projection shapes of one layer, weights rotating over "
                         "> 256 MB (from HBM)",
             "per_shape": res, "layer_us": tot_t * 1e6, "TOPS": tot_ops / tot_t / 1e12,
             "frac_mfma": tot_ops / tot_t / I8_PEAK,
             "layer_batched": {"launches": 4, "us": lt * 1e6, "us_range": [llo * 1e6, lhi * 1e6],
                               "TOPS": tot_ops / lt / 1e12, "frac_mfma": tot_ops / lt / I8_PEAK,
-                              "note": "q/k/v and gate/up each share one launch"},
+                              "note": "q/k/v and gate/up each share one launch",
+                              "us_one_copy": l1 * 1e6},
             "tokens_per_s_30_layers": 256 / (30 * lt)}
 
 
@@ -340,26 +346,36 @@ def extra_cfg4(gpu):
         N, K = next((N, K) for nm, N, K in LAYER if nm == name)
         return (bits, 8, N, K, pa, qs, L[name][0], L[name][1], outs[name])
 
-    def step(_i):
+    def step(_i, prep=True):
         # the reference forward's GEMM sequence per layer (forward.rs:484-641):
         # q/k/v on one activation, o, gate/up on one activation, down
         x, qs, pa = a2
         xd, qsd, pad_ = a8
         for L in layers:
-            gpu.prep(x, qs, pa, 8, 2048)                  # attention input
+            if prep:
+                gpu.prep(x, qs, pa, 8, 2048)              # attention input
             gpu.gemm_many([w(L, "q", 4, pa, qs), w(L, "k", 4, pa, qs), w(L, "v", 4, pa, qs)])
-            gpu.prep(x, qs, pa, 8, 2048)                  # attention output
+            if prep:
+                gpu.prep(x, qs, pa, 8, 2048)              # attention output
             gpu.gemm_many([w(L, "o", 4, pa, qs)])
-            gpu.prep(x, qs, pa, 8, 2048)                  # FFN input
+            if prep:
+                gpu.prep(x, qs, pa, 8, 2048)              # FFN input
             gpu.gemm_many([w(L, "gate", 4, pa, qs), w(L, "up", 4, pa, qs)])
-            gpu.prep(xd, qsd, pad_, 8, 8192)             # FFN hidden
+            if prep:
+                gpu.prep(xd, qsd, pad_, 8, 8192)         # FFN hidden
             gpu.gemm_many([w(L, "down", 8, pad_, qsd)])
-        gpu.prep(x, qs, pa, 8, 2048)
+        if prep:
+            gpu.prep(x, qs, pa, 8, 2048)
         gpu.q8c(8, 262144, 2048, pa, qs, head[0], head[1], logits)
 
     gs = gpu.graphs(step, 1, 1)
     gpu.time_graphs(gs, 3)
     dt, lo, hi = med_range(gpu.time_each(gs, 20))
+    # GEMM-only, as the reference's bench also times it (the packed
+    # activations the preps above left behind)
+    gg = gpu.graphs(lambda i: step(i, prep=False), 1, 1)
+    gpu.time_graphs(gg, 3)
+    gt, glo, ghi = med_range(gpu.time_each(gg, 20))
     wbytes = 0
     for name, N, K in LAYER:
         wbytes += (N * K + N * 4) if name == "down" else (N * K // 2 + (K // 64) * N * 2)
@@ -371,6 +387,8 @@ def extra_cfg4(gpu):
     return {"workload": "decode step M=8: 30 layers + int8 LM head, 242 launches (q/k/v and "
                         "gate/up batched), one graph",
             "us_per_step": dt * 1e6, "us_range": [lo * 1e6, hi * 1e6], "weight_bytes": wbytes,
+            "gemm_only": {"launches": 121, "us_per_step": gt * 1e6, "us_range": [glo * 1e6, ghi * 1e6],
+                          "GB_s_weights": wbytes / gt / 1e9},
             "GB_s_weights": wbytes / dt / 1e9,
             "GB_s_all": allb / dt / 1e9, "frac_hbm": allb / dt / HBM_PEAK,
             "tokens_per_s": 8 / dt}
@@ -1122,14 +1140,18 @@ def summary(out):
     if "per_shape" in c3:
         sm["cfg3_us"] = {k: _r(v["us"]) for k, v in c3["per_shape"].items()}
         lb = c3["layer_batched"]
-        sm["cfg3_layer"] = {"us": _r(lb["us"]), "range": _r(lb.get("us_range")), "frac_mfma": _r(lb["frac_mfma"])}
+        sm["cfg3_layer"] = {"us": _r(lb["us"]), "range": _r(lb.get("us_range")), "frac_mfma": _r(lb["frac_mfma"]),
+                            "us_one_copy": _r(lb.get("us_one_copy"))}
         if "cfg3" in per:
             sm["cfg3_layer"]["cpu_ms"] = _r(per["cfg3"]["layer"]["gemm"]["median_ms"])
     c4 = ex.get("cfg4", {})
     if "us_per_step" in c4:
         sm["cfg4"] = {"us": _r(c4["us_per_step"]), "frac_hbm": _r(c4["frac_hbm"]), "tok_s": _r(c4["tokens_per_s"])}
+        if "gemm_only" in c4:
+            sm["cfg4"]["gemm_only_us"] = _r(c4["gemm_only"]["us_per_step"])
         if "cfg4" in per:
             sm["cfg4"]["cpu_ms"] = _r(per["cfg4"]["prep_gemm"]["median_ms"])
+            sm["cfg4"]["cpu_gemm_only_ms"] = _r(per["cfg4"]["gemm"]["median_ms"])
     c5 = ex.get("cfg5", {})
     if "per_shape" in c5:
         sm["cfg5"] = {k: {"us": _r(v["us"]), "frac_mfma": _r(v["frac_mfma"])} for k, v in c5["per_shape"].items()}

@@ -155,8 +155,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   // ROT (int8, whose int32 sum is exact in any k order): workgroup b walks K
   // from k-block 5 b mod KB, so the tiles that share A rows or B columns read
   // different k-blocks at a time instead of the same lines at once (M = 256,
-  // N = 2048, K = 8192: 15.7 -> 13.2 us; for M = 2048 the shared lines are
-  // what the L2 reuses, and the rotation doubles the time)
+  // N = 2048, K = 8192, weights rotating over 20 copies: 15.9 -> 15.6 us;
+  // 15.8 -> 13.7 us in a bare stream of launches on constant-filled
+  // operands; for M = 2048 the shared lines are what the L2 reuses, and the
+  // rotation doubles the time)
   static_assert(!ROT || BITS == 8, "k rotation: int8 only");
   const int rot = ROT ? (int)((uint32_t)bid * 5u % (uint32_t)KB) : 0;
   // loads of k-block j of the group's stage sidx (k-blocks KS * (KW * sidx +
@@ -508,7 +510,7 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256;
   // M = 2048 down, K = 8192: 42.4 -> 38.9 us).  Long K keeps more stages in
   // flight: one k-block per stage, four or five stages per K group (M = 2048
-  // down 34.8 -> 31.0 us; M = 256 down with the k rotation 15.7 -> 13.2 us).
+  // down 34.8 -> 31.0 us; M = 256 down with the k rotation 15.9 -> 15.6 us).
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
     if (tiles(in, 128, 128) >= 240)  // long K (the down projection): two K groups
