@@ -56,6 +56,9 @@ def _bind(L: _C.CDLL) -> None:
     L.fgm_hip_available.restype = i
     L.fgm_hip_init.argtypes = [i]
     L.fgm_hip_gemm_path.argtypes = [i, i, i, i]
+    L.fgm_hip_gemm_plan.argtypes = [i, i, i, i, i, i, i, _C.POINTER(i)]
+    L.fgm_hip_weight_cache_bytes.argtypes = [i]
+    L.fgm_hip_weight_cache_bytes.restype = _C.c_size_t
     dev_q8c = [i, i, i, p, p, p, p, p, i, i, i, p]
     dev_q4g = [i, i, i, p, p, p, p, i, p, i, i, i, p]
     L.fgm_hip_gemm_q8c_dev.argtypes = dev_q8c
@@ -148,7 +151,7 @@ def _bind(L: _C.CDLL) -> None:
                  "fgm_hip_prep_rmsnorm_dev", "fgm_hip_prep_gelu_mul_dev", "fgm_hip_gemm_q8c_dev",
                  "fgm_hip_gemm_q4g_dev", "fgm_hip_acc_q8c_dev",
                  "fgm_hip_acc_q4g_dev", "fgm_hip_prep_rows_dev", "fgm_hip_quant_act_dev",
-                 "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path",
+                 "fgm_hip_pack_a_dev", "fgm_hip_fwht_dev", "fgm_hip_init", "fgm_hip_gemm_path", "fgm_hip_gemm_plan",
                  "fgm_hip_rmsnorm_dev", "fgm_hip_gelu_mul_dev", "fgm_hip_softcap_dev",
                  "fgm_hip_rope_dev", "fgm_hip_add_dev", "fgm_hip_mul_dev", "fgm_hip_scale_dev"):
         getattr(L, name).restype = i

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <shared_mutex>
 #include <unordered_map>
@@ -192,10 +193,19 @@ bool needs_chunks(int bits, const GemmProb& p) {
   return b_span(bits, p) > FGM_B_CHUNK && (p.n0 > 0 || p.nblocks > 1);
 }
 
+// Set by fgm_hip_gemm_plan on its own thread: run_probs then counts the
+// launch calls it would make instead of making them.
+thread_local int* g_plan = nullptr;
+
 int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
   GemmBatch sk{}, de{};
   auto flush = [&](GemmBatch& b, int dense) -> int {
     if (!b.count) return FGM_HIP_OK;
+    if (g_plan) {
+      ++*g_plan;
+      b.count = 0;
+      return FGM_HIP_OK;
+    }
     hipError_t e = dense ? fgm_launch_gemm(bits, b, st) : fgm_launch_decode(bits, b, st);
     b.count = 0;
     if (e != hipSuccess) return hip_fail(e, dense ? "dense GEMM launch" : "skinny GEMM launch");
@@ -211,7 +221,9 @@ int run_probs(int bits, const GemmProb* probs, int count, hipStream_t st) {
       return fail(FGM_HIP_EINVAL, "gemm: a_scale or b_scale is NULL");
     if (p.K == 0) {
       // a fill kernel, not a memset: this path may be captured into a graph
-      if (!p.acc_out) {
+      if (!p.acc_out && g_plan) {
+        ++*g_plan;
+      } else if (!p.acc_out) {
         hipError_t e = fgm_launch_fill_zero(p.C + 16 * p.n0, p.ldc, p.M, 16 * p.nblocks, st);
         if (e != hipSuccess) return hip_fail(e, "zero fill launch");
       }
@@ -268,14 +280,18 @@ struct CachedBuf {
   size_t bytes;
   uint64_t fp;
   void* dev;
+  // drop-in calls holding this copy (from the upload until their stream has
+  // drained)
+  std::atomic<int> users{0};
 };
 struct WeightCache {
   std::shared_mutex mu;
-  std::unordered_map<const void*, CachedBuf> map;
-  // copies replaced after a fingerprint mismatch: another thread may have
-  // been handed the old device pointer and still be launching on it, so it
-  // is freed only by fgm_hip_weight_cache_clear()
-  std::vector<void*> retired;
+  std::unordered_map<const void*, CachedBuf*> map;
+  // copies replaced after a fingerprint mismatch (a caller freed a weight
+  // buffer and reused its address): another thread may still be running on
+  // the old copy, so it is freed once no call holds it -- at the next
+  // upload, or by fgm_hip_weight_cache_clear()
+  std::vector<CachedBuf*> retired;
 } g_wcache;
 
 uint64_t fingerprint(const void* host, size_t bytes) {
@@ -290,33 +306,71 @@ uint64_t fingerprint(const void* host, size_t bytes) {
   return h;
 }
 
-int cached_upload(const void* host, size_t bytes, void** dev) {
+// The device copy of a host buffer, held for the caller (users + 1) until
+// it calls release_copy.
+int cached_upload(const void* host, size_t bytes, CachedBuf** out) {
   const uint64_t fp = fingerprint(host, bytes);
   {
     std::shared_lock<std::shared_mutex> lk(g_wcache.mu);
     auto it = g_wcache.map.find(host);
-    if (it != g_wcache.map.end() && it->second.bytes == bytes && it->second.fp == fp) {
-      *dev = it->second.dev;
+    if (it != g_wcache.map.end() && it->second->bytes == bytes && it->second->fp == fp) {
+      it->second->users++;
+      *out = it->second;
       return FGM_HIP_OK;
     }
   }
   std::unique_lock<std::shared_mutex> lk(g_wcache.mu);
   auto it = g_wcache.map.find(host);
   if (it != g_wcache.map.end()) {
-    if (it->second.bytes == bytes && it->second.fp == fp) {
-      *dev = it->second.dev;
+    if (it->second->bytes == bytes && it->second->fp == fp) {
+      it->second->users++;
+      *out = it->second;
       return FGM_HIP_OK;
     }
-    g_wcache.retired.push_back(it->second.dev);
+    g_wcache.retired.push_back(it->second);
     g_wcache.map.erase(it);
+  }
+  // free the retired copies no call holds any more
+  for (size_t i = 0; i < g_wcache.retired.size();) {
+    CachedBuf* r = g_wcache.retired[i];
+    if (r->users.load() == 0) {
+      (void)hipFree(r->dev);
+      delete r;
+      g_wcache.retired[i] = g_wcache.retired.back();
+      g_wcache.retired.pop_back();
+    } else {
+      i++;
+    }
   }
   void* d = nullptr;
   HIPCHK(hipMalloc(&d, bytes ? bytes : 1));
-  HIPCHK(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice));
-  g_wcache.map[host] = CachedBuf{bytes, fp, d};
-  *dev = d;
+  hipError_t e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return hip_fail(e, "weight upload");
+  }
+  CachedBuf* c = new CachedBuf;
+  c->bytes = bytes;
+  c->fp = fp;
+  c->dev = d;
+  c->users = 1;
+  g_wcache.map[host] = c;
+  *out = c;
   return FGM_HIP_OK;
 }
+
+// Drops a drop-in call's hold on the copies it used, once the stream its
+// launches went to has drained.
+struct CopyHold {
+  CachedBuf* c[2] = {nullptr, nullptr};
+  hipStream_t st = nullptr;
+  ~CopyHold() {
+    if (!c[0] && !c[1]) return;
+    if (st) (void)hipStreamSynchronize(st);
+    for (CachedBuf* x : c)
+      if (x) x->users--;
+  }
+};
 
 // Per-thread stream and grow-only staging buffers for the drop-ins: device
 // buffers, and pinned host buffers through which the caller's (pageable)
@@ -406,9 +460,14 @@ int dropin_gemm(int bits, int m, int n, int k, const int8_t* a, const float* a_s
   if (m == 0 || n1 == n0) return FGM_HIP_OK;
   const size_t bbytes = bits == 8 ? (size_t)n * k : (size_t)n * k / 2;
   const size_t sbytes = bits == 8 ? (size_t)n * 4 : (size_t)(k / group) * n * 2;
-  void *db = nullptr, *ds = nullptr, *da = nullptr, *das = nullptr, *dc = nullptr;
-  if ((rc = cached_upload(b, bbytes, &db))) return rc;
-  if ((rc = cached_upload(b_scale, sbytes, &ds))) return rc;
+  void *da = nullptr, *das = nullptr, *dc = nullptr;
+  CopyHold hold;
+  if (!g_stage.st) HIPCHK(hipStreamCreate(&g_stage.st));
+  hold.st = g_stage.st;
+  if ((rc = cached_upload(b, bbytes, &hold.c[0]))) return rc;
+  if ((rc = cached_upload(b_scale, sbytes, &hold.c[1]))) return rc;
+  void* db = hold.c[0]->dev;
+  void* ds = hold.c[1]->dev;
   const size_t abytes = packed_a_len(m, k);
   const int wcols = 16 * (n1 - n0);
   const size_t cbytes = (size_t)m * wcols * 4;
@@ -489,6 +548,23 @@ int fgm_hip_init(int device) {
 int fgm_hip_available(void) { return ensure_device() == FGM_HIP_OK ? 1 : 0; }
 
 int fgm_hip_gemm_path(int bits, int m, int k, int group) { return gemm_path(bits, m, k, group); }
+
+int fgm_hip_gemm_plan(int bits, int m, int n, int k, int group, int n0, int n1, int* launches) {
+  if (!launches) return fail(FGM_HIP_EINVAL, "gemm_plan: launches is NULL");
+  if (bits != 4 && bits != 8) return fail(FGM_HIP_EINVAL, "gemm_plan: bits=%d", bits);
+  int rc = check_gemm(m, n, k, n, n0, n1, bits, group);
+  if (rc) return rc;
+  // stand-in operand addresses: the dry run computes addresses and reads none
+  const uintptr_t fake = (uintptr_t)1 << 44;
+  GemmProb p = make_prob(m, n, k, (const int8_t*)fake, (const float*)fake, (const void*)fake,
+                         (const void*)fake, group, (float*)fake, n, n0, n1, nullptr, 0);
+  int count = 0;
+  g_plan = &count;
+  rc = run_probs(bits, &p, 1, nullptr);
+  g_plan = nullptr;
+  *launches = count;
+  return rc;
+}
 
 int fgm_hip_gemm_q8c_dev(int m, int n, int k, const int8_t* a, const float* a_scale,
                          const int8_t* b, const float* b_scale, float* c, int ldc, int n0, int n1,
@@ -659,13 +735,30 @@ int fgm_hip_fwht_dev(float* x, int n, int hsz, void* stream) {
 }
 
 // ---------------------------------------------------------------- drop-ins
+size_t fgm_hip_weight_cache_bytes(int replaced) {
+  std::shared_lock<std::shared_mutex> lk(g_wcache.mu);
+  size_t t = 0;
+  if (replaced) {
+    for (CachedBuf* r : g_wcache.retired) t += r->bytes;
+  } else {
+    for (auto& kv : g_wcache.map) t += kv.second->bytes;
+  }
+  return t;
+}
+
 void fgm_hip_weight_cache_clear(void) {
   std::unique_lock<std::shared_mutex> lk(g_wcache.mu);
   // callers clear the cache when no drop-in call is in flight; the device is
   // synchronised so that no queued kernel still reads a freed copy
   (void)hipDeviceSynchronize();
-  for (auto& kv : g_wcache.map) (void)hipFree(kv.second.dev);
-  for (void* d : g_wcache.retired) (void)hipFree(d);
+  for (auto& kv : g_wcache.map) {
+    (void)hipFree(kv.second->dev);
+    delete kv.second;
+  }
+  for (CachedBuf* r : g_wcache.retired) {
+    (void)hipFree(r->dev);
+    delete r;
+  }
   g_wcache.map.clear();
   g_wcache.retired.clear();
 }

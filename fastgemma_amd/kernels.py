@@ -244,6 +244,17 @@ def gemm_path(bits: int, m: int, k: int, group: int = 64) -> str:
     return ("skinny", "dense")[lib().fgm_hip_gemm_path(bits, m, k, group)]
 
 
+def gemm_plan(bits: int, m: int, n: int, k: int, group: int = 64, n0: int = 0, n1=None) -> int:
+    """Launch calls one GEMM of this shape makes (host-only dry run of the
+    dispatch, with the drop-ins' shape validation; raises FgmHipError on a
+    shape they refuse)."""
+    import ctypes
+    out = ctypes.c_int(-1)
+    check(lib().fgm_hip_gemm_plan(bits, m, n, k, group, n0, n // 16 if n1 is None else n1,
+                                  ctypes.byref(out)))
+    return out.value
+
+
 # ------------------------------------------------------ elementwise ops
 # lib.rs:220-291.  Host (numpy) buffers go to the drop-ins, GPU tensors to the
 # device API on torch's current stream.

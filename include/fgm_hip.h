@@ -88,6 +88,12 @@ int fgm_hip_available(void);
  * unmap or rewrite a weight file). */
 void fgm_hip_weight_cache_clear(void);
 
+/* Device bytes the weight cache holds: replaced = 0, the current copies;
+ * replaced = 1, copies replaced after a buffer was rewritten at the same
+ * address that a call still held at the last upload (freed at the next
+ * one).  No counterpart in the reference: memory accounting for callers. */
+size_t fgm_hip_weight_cache_bytes(int replaced);
+
 /* ======================================================= device-resident */
 
 /* Select and check the device (gfx950).  Optional: every entry point
@@ -337,6 +343,14 @@ int fgm_hip_linear_run_noalloc_dev(const fgm_hip_linear *w, const float *a, int 
 /* Which kernel family a GEMM of m rows runs on: 0 = skinny weight-stream
  * kernel, 1 = dense MFMA kernel. */
 int fgm_hip_gemm_path(int bits, int m, int k, int group);
+
+/* Dry run of one GEMM's dispatch, host only (no device is touched, no
+ * operand is read): validates the shape as fgm_hip_gemm_q8c_dev /
+ * fgm_hip_gemm_q4g_dev do and stores in *launches how many kernel launch
+ * calls the library would make for it (weights past 1 GiB are cut along N
+ * into several).  No counterpart in the reference: a planning query for
+ * tests and for callers that size graphs. */
+int fgm_hip_gemm_plan(int bits, int m, int n, int k, int group, int n0, int n1, int *launches);
 
 /* ------------------------------------------------------------ batched calls
  * No single reference counterpart: one call for the GEMMs a forward pass

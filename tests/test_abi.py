@@ -137,3 +137,28 @@ def test_skinny_dense_dispatch_thresholds():
     assert K.gemm_path(4, 256, 2048, 64) == "dense"
     # the int4 skinny kernel keeps every group's sums in LDS; past 160 KB it goes dense
     assert K.gemm_path(4, 64, 65536, 64) == "dense"
+
+
+def test_gemm_plan_cuts_weights_past_1gib():
+    """The GEMM dispatch's cuts along N, checked on the host alone (a dry run:
+    no device, no operand read): weights up to 1 GiB go in one launch, larger
+    ones in launches of at most 1 GiB, and an int8 n-block that alone passes
+    1 GiB (K > 2^26) is launched whole -- the case that once recursed without
+    end on the host.  The int4 cut covers the scale table's rebased columns
+    (the GPU side of both cuts: test_edge_gpu.py)."""
+    assert K.gemm_plan(4, 8, 8192, 2048) == 1                     # cfg2 up
+    assert K.gemm_plan(8, 8, 262144, 2048) == 1                   # LM head, 512 MiB
+    assert K.gemm_plan(8, 8, 524288, 2048) == 1                   # exactly 1 GiB
+    assert K.gemm_plan(8, 8, 524288 + 64, 2048) == 2              # 1 GiB + 4 n-blocks
+    assert K.gemm_plan(4, 8, 163840, 16384, 64) == 2              # int4 1.25 GiB, skinny
+    assert K.gemm_plan(4, 128, 163840, 16384, 64) == 2            # the same, dense
+    kl = (1 << 26) + 64                                           # one n-block: 1 GiB + 1 KiB
+    assert K.gemm_plan(8, 8, 64, kl) == 4
+    assert K.gemm_plan(8, 8, 128, kl, 64, 4, 8) == 4              # a range not at n-block 0
+    assert K.gemm_plan(8, 16, 64, kl) == 4                        # 16 rows: packed A 1 GiB
+    assert K.gemm_plan(8, 0, 8192, 2048) == 0                     # nothing to do
+    assert K.gemm_plan(8, 8, 8192, 0) == 1                        # k = 0: one zero fill
+    with pytest.raises(F.FgmHipError):
+        K.gemm_plan(8, 8, 64, 1 << 27)                            # packed A reaches 2^31
+    with pytest.raises(F.FgmHipError):
+        K.gemm_plan(4, 8, 8192, 2048, 96)                         # bad group

@@ -242,6 +242,27 @@ def test_dropin_host_pointer_api():
     assert np.array_equal(ap, oracle.pack_a(37, 192, a.reshape(37, 192)))
 
 
+def test_dropin_replaced_weights_are_reclaimed():
+    """A weight buffer rewritten again and again at one address: every call
+    sees the current contents, and each copy the cache replaces is freed at
+    the next upload once no call holds it, so the cache keeps one copy of
+    the buffer, not one per rewrite."""
+    import fastgemma_amd as F
+    from fastgemma_amd import kernels
+    L = F.lib()
+    M, N, Kd = 1, 4096, 4096                       # 16 MiB of int8 weights
+    A, Ap, a_s, B, bs = _inputs("q8c", M, N, Kd, 64, seed=47)
+    live = []
+    for rep in range(6):
+        B[:] = oracle.gen_i8(500 + rep, N * Kd, -127, 127)   # same address, new contents
+        C = np.zeros((M, N), np.float32)
+        kernels.gemm_q8c(M, N, Kd, Ap, a_s, B, bs, C, N, 0, N // 16)
+        assert _bits_equal(C, _oracle("q8c", M, N, Kd, Ap, a_s, B, bs, 64, 0, N // 16)), rep
+        assert L.fgm_hip_weight_cache_bytes(1) == 0, rep   # the replaced copy is gone
+        live.append(L.fgm_hip_weight_cache_bytes(0))
+    assert len(set(live)) == 1 and live[0] >= N * Kd, live
+
+
 # --------------------------------------------- live reference (if present)
 needs_ref = pytest.mark.skipif(oracle.ref() is None,
                                reason="oracle/_ref not present or host lacks AVX-512 VNNI")
