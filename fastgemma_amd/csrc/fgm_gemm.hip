@@ -508,9 +508,12 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // bounded rate (about 16 GB/s per wave from L2 on MI355X), so a small tile
   // needs more waves streaming it, and each group walks a quarter or half of
   // K (q 7.5 -> 6.9 us, down 19 -> 13 us, q + k + v 9.1 -> 7.6 us at M = 256;
-  // M = 2048 down, K = 8192: 42.4 -> 38.9 us).  Long K keeps more stages in
-  // flight: one k-block per stage, four or five stages per K group (M = 2048
-  // down 34.8 -> 31.0 us; M = 256 down with the k rotation 15.9 -> 15.6 us).
+  // M = 2048 down, K = 8192: 42.4 -> 38.9 us).  One k-block per stage, four
+  // stages per K group, for long K and for the 64x32 tiles (M = 2048 down
+  // 34.8 -> 31.0 us; M = 256 q 7.4 -> 7.2 us, down 15.7 -> 15.4 us, weights
+  // from HBM; the k rotation on the down projection 15.9 -> 15.6 us).  Eight
+  // K groups of 16 waves, or the 128x64 tile on eight 32x32 waves, measured
+  // slower (q 8.4, gate 12.9 us).
   if (bits == 8) {
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
     if (tiles(in, 128, 128) >= 240)  // long K (the down projection): two K groups
@@ -518,8 +521,8 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
                               : launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
     if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
     if (tiles(in, 64, 64) >= 160) return launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
-    return kmin(in) >= 8192 ? launch_any<8, 1, 1, 2, 1, 5, 1, 4, true>(in, st)
-                            : launch_any<8, 1, 1, 2, 1, 3, 2, 4>(in, st);
+    return kmin(in) >= 8192 ? launch_any<8, 1, 1, 2, 1, 4, 1, 4, true>(in, st)
+                            : launch_any<8, 1, 1, 2, 1, 4, 1, 4>(in, st);
   }
   if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
   if (tiles(in, 128, 64) >= 240) return launch_any<4, 2, 1, 2, 2, 2, 2>(in, st);
