@@ -105,7 +105,7 @@ __device__ __forceinline__ size_t pa_off(int row, int col, int KB) {
 // bound checks: float4s past the row read 0 through the buffer range check,
 // stay 0 through every stage (the rotation's blocks past k hold only them),
 // do not move the maximum, and their stores fall outside the store ranges.
-template <int PRE, int NV>
+template <int PRE, int NV, bool ROT, bool FAST>
 __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf, float* red) {
   const int k = a.k, KB = k >> 6;
   const int T = blockDim.x, tid = threadIdx.x;
@@ -113,7 +113,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   // 1. the row into registers
   const float* src = a.src + (size_t)row * a.lda;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)k * 4);
-  const bool vec = ((((uintptr_t)a.src) & 15) == 0) && (a.lda & 3) == 0 && (k & 3) == 0;
+  const bool vec = FAST || (((((uintptr_t)a.src) & 15) == 0) && (a.lda & 3) == 0 && (k & 3) == 0);
   float x[NV][4];
   if (vec) {
 #pragma unroll
@@ -140,7 +140,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
     float w[NV][4];
     if (a.aux) {
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.aux, (uint32_t)k * 4);
-      const bool wvec = (((uintptr_t)a.aux) & 15) == 0;
+      const bool wvec = FAST || (((uintptr_t)a.aux) & 15) == 0;
 #pragma unroll
       for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
@@ -192,7 +192,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   }
   if constexpr (PRE == PREP_GELU_MUL) {
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.aux + (size_t)row * a.lda, (uint32_t)k * 4);
-    const bool uvec = ((((uintptr_t)a.aux) & 15) == 0) && (a.lda & 3) == 0;
+    const bool uvec = FAST || (((((uintptr_t)a.aux) & 15) == 0) && (a.lda & 3) == 0);
 #pragma unroll
     for (int v = 0; v < NV; v++) {
       const int c = 4 * (tid + v * T);
@@ -213,7 +213,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   if constexpr (PRE != PREP_COPY) {
     if (a.pre) {
       const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.pre + (size_t)row * k, (uint32_t)k * 4);
-      const bool ovec = (((uintptr_t)a.pre) & 15) == 0;
+      const bool ovec = FAST || (((uintptr_t)a.pre) & 15) == 0;
 #pragma unroll
       for (int v = 0; v < NV; v++) {
         const int c = 4 * (tid + v * T);
@@ -238,7 +238,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   //    one wave, 256 and up go through LDS.  Each stage is one add (lower
   //    element) or one subtract (upper element) of the same two values in
   //    every schedule, so the bytes are the reference's.
-  if (a.hsz > 0) {
+  if (ROT && a.hsz > 0) {
     const int hsz = a.hsz;
     const int lane = tid & 63;
     if (hsz > 1) {
@@ -320,7 +320,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
 
   // 4. quantise and store: vector part [0, k & ~15) as _mm512_cvtps_epi32 +
   //    saturation, the scalar tail as lrintf + clamp (ops.c:194-203)
-  if ((k & 15) == 0) {
+  if (FAST || (k & 15) == 0) {
     // the whole row in vector form: one dword of int8 per float4, stores
     // past the row dropped by the range check.  The packed tile row of
     // `row` is 64 bytes every 1024: [row/16][k/64][row%16][k%64].
@@ -387,7 +387,7 @@ __device__ __forceinline__ void prep_row(const PrepProb& a, int row, float* buf,
   }
 }
 
-template <int PRE>
+template <int PRE, bool ROT, bool FAST, int NVK>
 __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch bt) {
   extern __shared__ float buf[];
   __shared__ __attribute__((aligned(16))) float red[PREP_MAX_THREADS / 64];
@@ -411,12 +411,18 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
     }
     return;
   }
-  // float4s per thread that reach into the row (uniform; the launcher keeps
-  // it within 1 .. VMAX)
-  const int nv = ((k + 3) / 4 + T - 1) / T;
-  sfor<1, VMAX + 1>([&](auto N) {
-    if (nv == N) prep_row<PRE, N>(a, row, buf, red);
-  });
+  if constexpr (NVK > 0) {
+    // one body for every row of the batch, NVK float4s per thread: those past
+    // a shorter row read 0 and store nothing
+    prep_row<PRE, NVK, ROT, FAST>(a, row, buf, red);
+  } else {
+    // float4s per thread that reach into the row (uniform; the launcher keeps
+    // it within 1 .. VMAX)
+    const int nv = ((k + 3) / 4 + T - 1) / T;
+    sfor<1, VMAX + 1>([&](auto N) {
+      if (nv == N) prep_row<PRE, N, ROT, FAST>(a, row, buf, red);
+    });
+  }
 }
 
 // fgm_pack_a (ops.c:279-290), 16 bytes per thread.
@@ -467,14 +473,44 @@ static hipError_t allow_big_lds(K kernel) {
                              160 * 1024 - 1024);
 }
 
+// One kernel per (producer, rotation compiled in, every operand aligned for
+// 16-byte access with k % 16 == 0, float4s per thread): a batch that needs
+// neither the rotation nor the unaligned and scalar-tail paths runs a single
+// straight-line row body.  At this kernel's sizes the code on the executed
+// path matters: it is fetched cold at every launch (a copy prep of 8 rows,
+// k = 8192: 3.57 us with every path in one kernel, 3.33 us without the
+// rotation, the unaligned loads and the scalar tail).
+template <int PRE, bool ROT, bool FAST, int NVK>
+static hipError_t launch_prep_kernel(const PrepBatch& b, int nwg, int threads, size_t lds, hipStream_t st) {
+  static hipError_t attr = allow_big_lds(prep_rows_kernel<PRE, ROT, FAST, NVK>);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((prep_rows_kernel<PRE, ROT, FAST, NVK>), dim3(nwg), dim3(threads), lds, st, b);
+  return hipGetLastError();
+}
+
+template <int PRE, bool ROT>
+static hipError_t launch_prep_rot(const PrepBatch& b, bool fast, int nvk, int nwg, int threads, size_t lds,
+                                  hipStream_t st) {
+  if (!fast) return launch_prep_kernel<PRE, ROT, false, 0>(b, nwg, threads, lds, st);
+  switch (nvk) {
+    case 1: return launch_prep_kernel<PRE, ROT, true, 1>(b, nwg, threads, lds, st);
+    case 2: return launch_prep_kernel<PRE, ROT, true, 2>(b, nwg, threads, lds, st);
+    case 4: return launch_prep_kernel<PRE, ROT, true, 4>(b, nwg, threads, lds, st);
+    default: return launch_prep_kernel<PRE, ROT, true, 8>(b, nwg, threads, lds, st);
+  }
+}
+
+template <int PRE>
+static hipError_t launch_prep_pre(const PrepBatch& b, bool rot, bool fast, int nvk, int nwg, int threads,
+                                  size_t lds, hipStream_t st) {
+  return rot ? launch_prep_rot<PRE, true>(b, fast, nvk, nwg, threads, lds, st)
+             : launch_prep_rot<PRE, false>(b, fast, nvk, nwg, threads, lds, st);
+}
+
 hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
-  static hipError_t attr[3] = {allow_big_lds(prep_rows_kernel<PREP_COPY>),
-                               allow_big_lds(prep_rows_kernel<PREP_RMSNORM>),
-                               allow_big_lds(prep_rows_kernel<PREP_GELU_MUL>)};
   PrepBatch b = in;
   const int pre = b.count ? b.p[0].preop : PREP_COPY;
   if (pre < PREP_COPY || pre > PREP_GELU_MUL) return hipErrorInvalidValue;
-  if (attr[pre] != hipSuccess) return attr[pre];
   int nwg = 0, kmax = 0, lds_floats = 0;
   for (int i = 0; i < b.count; i++) {
     PrepProb& p = b.p[i];
@@ -504,13 +540,21 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
   // the kernel has a row body for 1 .. VMAX float4s per thread only
   if (((kmax + 3) / 4 + threads - 1) / threads > VMAX) return hipErrorInvalidValue;
   const size_t lds = (size_t)lds_floats * sizeof(float);
-  if (pre == PREP_RMSNORM)
-    hipLaunchKernelGGL(prep_rows_kernel<PREP_RMSNORM>, dim3(nwg), dim3(threads), lds, st, b);
-  else if (pre == PREP_GELU_MUL)
-    hipLaunchKernelGGL(prep_rows_kernel<PREP_GELU_MUL>, dim3(nwg), dim3(threads), lds, st, b);
-  else
-    hipLaunchKernelGGL(prep_rows_kernel<PREP_COPY>, dim3(nwg), dim3(threads), lds, st, b);
-  return hipGetLastError();
+  bool rot = false, fast = true;
+  for (int i = 0; i < b.count; i++) {
+    const PrepProb& p = b.p[i];
+    if (p.r0 >= p.r1) continue;
+    rot = rot || p.hsz > 0;
+    fast = fast && ((uintptr_t)p.src & 15) == 0 && (p.lda & 3) == 0 && (p.k & 15) == 0 &&
+           ((uintptr_t)p.aux & 15) == 0 && ((uintptr_t)p.pre & 15) == 0;
+  }
+  // the fast kernels' body: the widest row's float4s per thread, rounded up
+  // to a power of two
+  const int nvmax = ((kmax + 3) / 4 + threads - 1) / threads;
+  const int nvk = nvmax <= 1 ? 1 : nvmax <= 2 ? 2 : nvmax <= 4 ? 4 : 8;
+  if (pre == PREP_RMSNORM) return launch_prep_pre<PREP_RMSNORM>(b, rot, fast, nvk, nwg, threads, lds, st);
+  if (pre == PREP_GELU_MUL) return launch_prep_pre<PREP_GELU_MUL>(b, rot, fast, nvk, nwg, threads, lds, st);
+  return launch_prep_pre<PREP_COPY>(b, rot, fast, nvk, nwg, threads, lds, st);
 }
 
 hipError_t fgm_launch_pack_a(int M, int K, const int8_t* A, int8_t* Ap, hipStream_t st) {
