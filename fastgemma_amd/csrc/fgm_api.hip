@@ -145,7 +145,7 @@ GemmProb make_prob(int m, int n, int k, const int8_t* a, const float* a_scale, c
   p.ldacc = ldacc;
   p.n0 = n0;
   p.nblocks = n1 - n0;
-  p.wg0 = 0;
+  p.nwg = 0;
   p.tw = p.ks = p.nbw = 0;
   return p;
 }

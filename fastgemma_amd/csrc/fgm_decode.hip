@@ -191,6 +191,8 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   constexpr int TPU = G::TPU, OUT = G::OUT, NA = G::NA, X = G::X, D = G::D;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick_problem(bt);
+  fetch_all(a);
+  if ((int)blockIdx.x >= a.nwg) return;  // past this problem's workgroups
   const int tid = threadIdx.x, NT = blockDim.x;
   const int w = wave_id(), l = tid & 63, g = l >> 4, j = l & 15;
   const int M = a.M, N = a.N, KB = a.K >> 6;
@@ -204,10 +206,12 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   // contiguous run of n-blocks, so that the workgroups sharing a 128-byte
   // line of group scales (four n-blocks) share an L2 and fetch it from HBM
   // once.  (int8 scales are one float per column, nothing is shared, and
-  // the interleaved order measured faster: cfg1 5.45 against 6.3 us.)
-  int lb = (int)blockIdx.x - a.wg0;
-  const int nwgp = (a.nblocks + NBW - 1) / NBW;
-  if (BITS == 4 && (a.wg0 & 7) == 0 && (nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
+  // the interleaved order measured faster: cfg1 5.45 against 6.3 us.)  The
+  // grid's width is a multiple of 8, so workgroup x of every problem runs on
+  // XCD x % 8.
+  int lb = (int)blockIdx.x;
+  const int nwgp = a.nwg;
+  if (BITS == 4 && (nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
   const int nb_first = a.n0 + lb * NBW;
   const int nb_here = min(NBW, a.n0 + a.nblocks - nb_first);
   const Lay L(BITS, OUT, D, KS, UPW, NWS, NBW, KB, Mp, PIR);
@@ -569,10 +573,11 @@ bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw, bool p
 
 template <int BITS, int MB, bool HALF, bool G1, bool RAW, bool PIR = false>
 hipError_t launch_variant(const GemmBatch& bt, int nw, size_t lds, int nwg, hipStream_t st) {
+  // one grid row per problem, as wide as the widest, a multiple of 8
   auto k = decode_kernel<BITS, MB, HALF, G1, RAW, PIR>;
   static hipError_t attr = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(k, dim3(nwg), dim3(nw * 64), lds, st, bt);
+  hipLaunchKernelGGL(k, dim3((nwg + 7) / 8 * 8, bt.count), dim3(nw * 64), lds, st, bt);
   return hipGetLastError();
 }
 
@@ -677,13 +682,12 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
     while (nbw > 1 && (nbw > p.nblocks || !fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir))) nbw /= 2;
     if (!fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir)) return hipErrorInvalidValue;
     p.nbw = nbw;
-    p.wg0 = nwg;
-    nwg += (p.nblocks + nbw - 1) / nbw;
+    p.nwg = (p.nblocks + nbw - 1) / nbw;
+    nwg = std::max(nwg, p.nwg);
     const size_t need = lay_for(bits, Mv, p.K, p.ks, NWS, nbw, pir).total;
     if (need > lds) lds = need;
   }
   if (nwg == 0) return hipSuccess;
-  close_batch(bt);
   // the kernel derives a problem's stream waves as KS * NBW; pad the others
   // up to the launch's NWS with idle n-blocks is not needed: every problem
   // uses NBW = NWS / KS unless its n-blocks run out

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick_problem(bt);
+  fetch_all(a);
   const int tid = threadIdx.x, wv = wave_id(), l = tid & 63, h = l >> 5, l32 = l & 31;
   // K group kg, wave w within it
   const int kg = wv / C::NWG, w = wv - kg * C::NWG;
@@ -93,11 +94,14 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   const int MT = (M + C::BM - 1) / C::BM;
   const int NT = (a.nblocks + C::NBL - 1) / C::NBL;
   const int ntiles = MT * NT;
-  int bid = blockIdx.x - a.wg0;
-  // Workgroup ids go round-robin over the 8 XCDs: give each XCD a contiguous
-  // run of tiles in grouped order (GM m-tiles at a time, n within a group),
-  // so that the tiles an L2 serves at once share A rows and B columns.
-  if ((ntiles & 7) == 0 && (a.wg0 & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+  int bid = blockIdx.x;
+  if (bid >= a.nwg) return;  // past this problem's tiles
+  // Workgroup ids go round-robin over the 8 XCDs (the grid's width is a
+  // multiple of 8, so workgroup x of every problem runs on XCD x % 8): give
+  // each XCD a contiguous run of tiles in grouped order (GM m-tiles at a
+  // time, n within a group), so that the tiles an L2 serves at once share A
+  // rows and B columns.
+  if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
   const int GM = MT < 4 ? MT : 4;
   const int grp = bid / (GM * NT), inr = bid - grp * GM * NT;
   const int gm = (MT - grp * GM) < GM ? (MT - grp * GM) : GM;  // m-tiles in this group
@@ -453,12 +457,12 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
     GemmProb& p = b.p[i];
     // the epilogue addresses one m-tile of C with 32-bit buffer offsets
     if ((size_t)C::BM * (size_t)(p.acc_out ? p.ldacc : p.ldc) * 4 > 0xFFFFFFFFull) return hipErrorInvalidValue;
-    p.wg0 = nwg;
-    nwg += ((p.M + C::BM - 1) / C::BM) * ((p.nblocks + C::NBL - 1) / C::NBL);
+    p.nwg = ((p.M + C::BM - 1) / C::BM) * ((p.nblocks + C::NBL - 1) / C::NBL);
+    nwg = nwg > p.nwg ? nwg : p.nwg;
   }
   if (nwg == 0) return hipSuccess;
-  close_batch(b);
-  hipLaunchKernelGGL(k, dim3(nwg), dim3(C::T), C::LDS, st, b);
+  // one grid row per problem, as wide as the widest, a multiple of 8
+  hipLaunchKernelGGL(k, dim3((nwg + 7) / 8 * 8, b.count), dim3(C::T), C::LDS, st, b);
   return hipGetLastError();
 }
 

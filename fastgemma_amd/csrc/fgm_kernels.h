@@ -9,25 +9,16 @@
 // Independent problems served by one launch.
 constexpr int FGM_MAX_BATCH = 4;
 
-// The problem workgroup blockIdx.x belongs to: problem i owns workgroups
-// [p[i].wg0, p[i + 1].wg0), and the launcher sets wg0 = INT_MAX in the slots
-// past the batch.  Every wg0 is read in one round of scalar loads and the
-// index is formed without branches, then the chosen problem is read by that
-// index: two dependent argument fetches at kernel start, not one per
-// problem (each is a memory round trip while the argument lines are cold).
+// Problem i of a batch is row blockIdx.y = i of a 2-D grid and owns its
+// workgroups blockIdx.x = 0 .. p[i].nwg - 1; the grid is as wide as the
+// widest problem and the others' surplus workgroups exit at once.  The
+// problem is read at an address every workgroup knows when it starts: one
+// round of argument fetches at kernel start, not a fetch to find the problem
+// and a second to read it (each is a memory round trip while the argument
+// lines are cold).
 template <class Batch>
 __device__ __forceinline__ auto pick_problem(const Batch& bt) {
-  const int b = blockIdx.x;
-  int i = 0;
-#pragma unroll
-  for (int k = 1; k < FGM_MAX_BATCH; k++) i += b >= bt.p[k].wg0 ? 1 : 0;
-  return bt.p[__builtin_amdgcn_readfirstlane(i)];
-}
-
-// wg0 of the slots past the batch (see pick_problem)
-template <class Batch>
-inline void close_batch(Batch& bt) {
-  for (int k = bt.count; k < FGM_MAX_BATCH; k++) bt.p[k].wg0 = 0x7FFFFFFF;
+  return bt.p[blockIdx.y];
 }
 
 struct GemmProb {
@@ -39,7 +30,7 @@ struct GemmProb {
   int32_t* acc_out;       // raw int32 accumulators instead of C when non-null
   int M, N, K, group, ldc, ldacc;
   int n0, nblocks;        // n-block range [n0, n0 + nblocks)
-  int wg0;                // first workgroup of this problem (set by the launcher)
+  int nwg;                // workgroups of this problem (set by the launcher)
   int tw, ks, nbw;        // skinny path: k-blocks per wave, waves per n-block,
                           // n-blocks per workgroup (set by the launcher)
 };
@@ -57,7 +48,7 @@ struct PrepProb {
   int8_t* pa;      // null for quant_act
   int lda, m, k, hsz, r0, r1;
   float fwht_scale;
-  int wg0;         // first workgroup (set by the launcher)
+  int nwg;         // workgroups of this problem (set by the launcher)
   // fused producer applied to each row before the rotation (one kind per
   // batch): PREP_RMSNORM normalises src by aux (NULL: no scale) with eps;
   // PREP_GELU_MUL takes gelu(src) * aux, aux rows lda apart.  pre, when set,
@@ -67,6 +58,21 @@ struct PrepProb {
   float* pre;
   float eps;
 };
+// Every field of the problem (and the workgroup size) in registers at once:
+// the kernels test whether a workgroup is past its problem first, and the
+// compiler would otherwise fetch the fields that test needs, branch, and
+// fetch the rest in a second dependent round.
+__device__ __forceinline__ void fetch_all(const GemmProb& a) {
+  asm volatile("" ::"s"(a.A), "s"(a.a_scale), "s"(a.B), "s"(a.b_scale), "s"(a.C), "s"(a.acc_out),
+               "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.group), "s"(a.ldc), "s"(a.ldacc), "s"(a.n0),
+               "s"(a.nblocks), "s"(a.nwg), "s"(a.tw), "s"(a.ks), "s"(a.nbw), "s"(blockDim.x));
+}
+__device__ __forceinline__ void fetch_all(const PrepProb& a) {
+  asm volatile("" ::"s"(a.src), "s"(a.rot), "s"(a.qa), "s"(a.qs), "s"(a.pa), "s"(a.lda), "s"(a.m),
+               "s"(a.k), "s"(a.hsz), "s"(a.r0), "s"(a.r1), "s"(a.fwht_scale), "s"(a.nwg),
+               "s"(a.preop), "s"(a.aux), "s"(a.pre), "s"(a.eps), "s"(blockDim.x));
+}
+
 enum { PREP_COPY = 0, PREP_RMSNORM = 1, PREP_GELU_MUL = 2 };
 
 struct PrepBatch {

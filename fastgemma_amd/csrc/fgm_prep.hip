@@ -392,7 +392,9 @@ __global__ __launch_bounds__(PREP_MAX_THREADS) void prep_rows_kernel(PrepBatch b
   extern __shared__ float buf[];
   __shared__ __attribute__((aligned(16))) float red[PREP_MAX_THREADS / 64];
   const PrepProb a = pick_problem(bt);
-  const int row = a.r0 + (blockIdx.x - a.wg0);
+  fetch_all(a);
+  if ((int)blockIdx.x >= a.nwg) return;  // past this problem's rows
+  const int row = a.r0 + (int)blockIdx.x;
   const int k = a.k, KB = k >> 6;
   const int T = blockDim.x, tid = threadIdx.x;
 
@@ -484,7 +486,8 @@ template <int PRE, bool ROT, bool FAST, int NVK>
 static hipError_t launch_prep_kernel(const PrepBatch& b, int nwg, int threads, size_t lds, hipStream_t st) {
   static hipError_t attr = allow_big_lds(prep_rows_kernel<PRE, ROT, FAST, NVK>);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((prep_rows_kernel<PRE, ROT, FAST, NVK>), dim3(nwg), dim3(threads), lds, st, b);
+  // one grid row per problem, as wide as the problem with the most rows
+  hipLaunchKernelGGL((prep_rows_kernel<PRE, ROT, FAST, NVK>), dim3(nwg, b.count), dim3(threads), lds, st, b);
   return hipGetLastError();
 }
 
@@ -515,11 +518,12 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
   for (int i = 0; i < b.count; i++) {
     PrepProb& p = b.p[i];
     if (p.preop != pre || (pre != PREP_COPY && p.k % 64)) return hipErrorInvalidValue;
-    p.wg0 = nwg;
+    p.nwg = 0;
     if (p.r0 < p.r1) {
       // rows [r0, r1) compute; rows [r1, end of r1's tile block) only pack
       const int end = p.pa ? ((p.r1 + 15) / 16) * 16 : p.r1;
-      nwg += end - p.r0;
+      p.nwg = end - p.r0;
+      nwg = std::max(nwg, p.nwg);
       if (p.k > kmax) kmax = p.k;
       if (p.hsz > 0 && p.k > lds_floats) lds_floats = p.k;
       // the transposed row plus 1/rms (16 S + 1 > k floats)
@@ -527,7 +531,6 @@ hipError_t fgm_launch_prep(const PrepBatch& in, hipStream_t st) {
     }
   }
   if (nwg == 0) return hipSuccess;
-  close_batch(b);
   // One float4 per thread up to 512 threads (gelu_mul, heavier per element:
   // 1024), more float4s per thread beyond, at most VMAX: a row's work is
   // latency-bound at the decode sizes, so more waves per row pay until the
