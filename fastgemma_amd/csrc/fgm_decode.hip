@@ -66,6 +66,7 @@ namespace {
 constexpr int MAX_WAVES = 16;
 constexpr int DPP_ROW_ROR8 = 0x128;
 constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thread
+constexpr int CHP = 8;            // group-64 chain: 4-k-tile chunks in flight
 #ifndef FGM_DEC_UPW
 #define FGM_DEC_UPW 4             // target units (1 KB) per stream wave
 #endif
@@ -103,6 +104,10 @@ FGM_DEV void pir_wait6(v2i (&p)[4], v4i (&sc)[2]) {
 }
 FGM_DEV void pir_wait0(v2i (&p)[4], v4i (&sc)[2]) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(sc[0]), "+v"(sc[1]) : : "memory");
+}
+template <int N>
+FGM_DEV void lgkm_wait(v4i& r0, v4i& r1) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(r0), "+v"(r1) : "n"(N) : "memory");
 }
 FGM_DEV void lgkm_wait6(v4i& r0, v4i& r1) {
   asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(r0), "+v"(r1) : : "memory");
@@ -178,6 +183,9 @@ struct Lay {
       const uint32_t ring_end = (uint32_t)nws * slots * 1024, need = ring_end + 3072 + 32;
       if (o < need) o = need;
     }
+    // the group-64 chain reads up to 2 CHP - 2 chunks of 16 bytes past the
+    // last scale row
+    if (bits == 4) o += 16 * (2 * CHP - 2);
     total = o;
   }
 };
@@ -220,7 +228,9 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
 
   // ---- the stream: this wave's weights (an empty range if it has no
   // n-block), packed A
-  const int q = w / KS, s = w - q * KS;            // wave's n-block, K slice
+  // KS and NBW are powers of two (the launcher's split): shifts, not divisions
+  const int lks = __builtin_ctz(KS), lnbw = __builtin_ctz(NBW);
+  const int q = w >> lks, s = w & (KS - 1);        // wave's n-block, K slice
   const bool live = w < NWP && q < nb_here;
   const int UPWw = w < NWP ? UPW : 0;              // units this wave streams
   const v4i rb = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (live ? q : 0)) * KB * TB,
@@ -270,7 +280,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
     const int per_g = 8 * NBW;  // dwords per group (two columns each)
 #pragma unroll
     for (int v = 0; v < SPT; v++) {
-      const int i = tid + v * NT, gi = i / per_g, c2 = i - gi * per_g, qq = c2 >> 3;
+      const int i = tid + v * NT, gi = i >> (3 + lnbw), c2 = i - gi * per_g, qq = c2 >> 3;
       const bool ok = gi < NG && qq < nb_here;
       sreg[v] = (uint32_t)buf_load_b32(rs, ok ? (uint32_t)((gi * N + (nb_first + qq) * 16 + 2 * (c2 & 7)) * 2) : FGM_OOB, 0);
     }
@@ -402,7 +412,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
       const int per_g = 8 * NBW;
 #pragma unroll
       for (int v = 0; v < SPT; v++) {
-        const int ii = tid + v * NT, gi = ii / per_g, c2 = ii - gi * per_g, qq = c2 >> 3;
+        const int ii = tid + v * NT, gi = ii >> (3 + lnbw), c2 = ii - gi * per_g, qq = c2 >> 3;
         if (gi < L.ngp && qq < NBW) {
           float* d = S + (qq * 16 + 2 * (c2 & 7)) * L.ngp + gi;
           const bool ok = gi < NG && qq < nb_here;
@@ -457,26 +467,30 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
         }
         a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
       } else if (G1 && !RAW) {
-        // group = k-tile: chunks of four; the next chunk's sums and scales are
-        // read (volatile: kept in place) before this chunk's fmas
-        // LDS reads by address (ds_read_b128 in inline asm, waited for with
-        // lgkmcnt): the compiler would otherwise sink the prefetch next to
-        // its use.  The sums are parked as floats.  Reads up to three chunks
-        // past a row stay inside the workgroup's LDS and are not used.
+        // group = k-tile: chunks of four, CHP - 1 chunks' sums and scales read
+        // ahead of the chunk being folded (the LDS round trip is longer than
+        // four dependent fmas; cfg2 pair 7.25 -> 7.2 us against 3 ahead).  The
+        // sums are parked as the floats the chain multiplies (converting them
+        // here instead put the conversion on the chain: 7.55 us).  LDS reads by address (ds_read_b128 in inline
+        // asm, waited for with lgkmcnt): the compiler would otherwise sink the
+        // prefetch next to its use.  Reads up to 2 CHP - 2 chunks past a row
+        // stay inside the workgroup's LDS (the layout's tail pad) and are not
+        // used.
         const uint32_t pa0 = lds0 + L.park + (uint32_t)((qq * OUT + oo) * L.pp) * 4u;
         const uint32_t sa0 = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
         const int nch = (KB + 3) >> 2;           // k-tiles past K hold zeros (parked or set above)
         float cacc = 0.0f;
-        v4i pv[4], sv[4];
-        lds_read2x128<0>(pv[0], sv[0], pa0, sa0);
-        lds_read2x128<16>(pv[1], sv[1], pa0, sa0);
-        lds_read2x128<32>(pv[2], sv[2], pa0, sa0);
-        for (int ch = 0; ch < nch; ch += 4) {
+        v4i pv[CHP], sv[CHP];
+        sfor<0, CHP - 1>([&](auto bc) {
+          constexpr int b = decltype(bc)::value;
+          lds_read2x128<16 * b>(pv[b], sv[b], pa0, sa0);
+        });
+        for (int ch = 0; ch < nch; ch += CHP) {
           const uint32_t pb = pa0 + 16u * ch, sb = sa0 + 16u * ch;
-          sfor<0, 4>([&](auto bc) {
+          sfor<0, CHP>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
-            lds_read2x128<16 * (b + 3)>(pv[(b + 3) & 3], sv[(b + 3) & 3], pb, sb);
-            lgkm_wait6(pv[b], sv[b]);
+            lds_read2x128<16 * (b + CHP - 1)>(pv[(b + CHP - 1) % CHP], sv[(b + CHP - 1) % CHP], pb, sb);
+            lgkm_wait<2 * (CHP - 1)>(pv[b], sv[b]);
             if (ch + b < nch) {
               cacc = __builtin_fmaf(__int_as_float(pv[b].x), __int_as_float(sv[b].x), cacc);
               cacc = __builtin_fmaf(__int_as_float(pv[b].y), __int_as_float(sv[b].y), cacc);
@@ -485,7 +499,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
             }
           });
         }
-        sfor<0, 4>([&](auto bc) { lgkm_wait0(pv[decltype(bc)::value], sv[decltype(bc)::value]); });
+        sfor<0, CHP>([&](auto bc) { lgkm_wait<0>(pv[decltype(bc)::value], sv[decltype(bc)::value]); });
         a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
       } else {
         // any group size, and the raw per-group sums
@@ -681,6 +695,8 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
     int nbw = NWS / p.ks;
     while (nbw > 1 && (nbw > p.nblocks || !fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir))) nbw /= 2;
     if (!fits_wg(bits, Mv, p.K, p.group, NWS, p.ks, nbw, pir)) return hipErrorInvalidValue;
+    // the kernel splits waves and scale dwords by shifts
+    if ((nbw & (nbw - 1)) || (p.ks & (p.ks - 1))) return hipErrorInvalidValue;
     p.nbw = nbw;
     p.nwg = (p.nblocks + nbw - 1) / nbw;
     nwg = std::max(nwg, p.nwg);
