@@ -485,20 +485,26 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
           constexpr int b = decltype(bc)::value;
           lds_read2x128<16 * b>(pv[b], sv[b], pa0, sa0);
         });
-        for (int ch = 0; ch < nch; ch += CHP) {
+        // whole blocks of CHP chunks, then the last, partial block with a
+        // per-chunk test (outside the blocks the test would put a select on
+        // the fma chain's dependence path)
+        auto block = [&](int ch, auto partial) {
           const uint32_t pb = pa0 + 16u * ch, sb = sa0 + 16u * ch;
           sfor<0, CHP>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
             lds_read2x128<16 * (b + CHP - 1)>(pv[(b + CHP - 1) % CHP], sv[(b + CHP - 1) % CHP], pb, sb);
             lgkm_wait<2 * (CHP - 1)>(pv[b], sv[b]);
-            if (ch + b < nch) {
+            if (!decltype(partial)::value || ch + b < nch) {
               cacc = __builtin_fmaf(__int_as_float(pv[b].x), __int_as_float(sv[b].x), cacc);
               cacc = __builtin_fmaf(__int_as_float(pv[b].y), __int_as_float(sv[b].y), cacc);
               cacc = __builtin_fmaf(__int_as_float(pv[b].z), __int_as_float(sv[b].z), cacc);
               cacc = __builtin_fmaf(__int_as_float(pv[b].w), __int_as_float(sv[b].w), cacc);
             }
           });
-        }
+        };
+        const int nfull = nch / CHP * CHP;
+        for (int ch = 0; ch < nfull; ch += CHP) block(ch, std::false_type{});
+        if (nfull < nch) block(nfull, std::true_type{});
         sfor<0, CHP>([&](auto bc) { lgkm_wait<0>(pv[decltype(bc)::value], sv[decltype(bc)::value]); });
         a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
       } else {
