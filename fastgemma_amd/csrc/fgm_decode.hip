@@ -66,7 +66,7 @@ namespace {
 constexpr int MAX_WAVES = 16;
 constexpr int DPP_ROW_ROR8 = 0x128;
 constexpr int SPT = 4;            // int4 group-scale dwords prefetched per thread
-constexpr int CHP = 8;            // group-64 chain: 4-k-tile chunks in flight
+constexpr int CHP = 4;            // group-64 chain: pairs of 4-k-tile chunks in flight
 #ifndef FGM_DEC_UPW
 #define FGM_DEC_UPW 4             // target units (1 KB) per stream wave
 #endif
@@ -105,6 +105,23 @@ FGM_DEV void pir_wait6(v2i (&p)[4], v4i (&sc)[2]) {
 FGM_DEV void pir_wait0(v2i (&p)[4], v4i (&sc)[2]) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(sc[0]), "+v"(sc[1]) : : "memory");
 }
+// Three 16-byte LDS reads (two at a0, a0 + 16 plus OA; one at a1 plus OB),
+// and a wait for all but the last N LDS operations that also orders the use
+// of the given registers after it.
+template <int OA, int OB>
+FGM_DEV void lds_read3x128(v4i& r0, v4i& r1, v4i& r2, uint32_t a0, uint32_t a1) {
+  asm volatile("ds_read_b128 %0, %3 offset:%5\n\tds_read_b128 %1, %3 offset:%6\n\tds_read_b128 %2, %4 offset:%7"
+               : "=&v"(r0), "=&v"(r1), "=&v"(r2)
+               : "v"(a0), "v"(a1), "n"(OA), "n"(OA + 16), "n"(OB)
+               : "memory");
+}
+template <int N>
+FGM_DEV void lgkm_wait3(v4i& r0, v4i& r1, v4i& r2) {
+  asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(r0), "+v"(r1), "+v"(r2) : "n"(N) : "memory");
+}
+// The f16 in the low / high half of a dword, widened (exactly) to f32.
+FGM_DEV float f16lo(int x) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(x & 0xFFFF)); }
+FGM_DEV float f16hi(int x) { return (float)__builtin_bit_cast(_Float16, (uint16_t)((uint32_t)x >> 16)); }
 template <int N>
 FGM_DEV void lgkm_wait(v4i& r0, v4i& r1) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(r0), "+v"(r1) : "n"(N) : "memory");
@@ -156,21 +173,26 @@ struct Geo {
 // park area is empty.
 struct Lay {
   uint32_t ring, park, scl, asc, bsc, total;
-  int slots, pp, ngp;
+  int slots, pp, ngp, ngh;
   __host__ __device__ Lay(int bits, int out, int d, int ks, int upw, int nws, int nbw, int kb, int mp,
                           bool pir = false) {
     const int tpu = bits == 4 ? 2 : 1;
     slots = upw < d ? upw : d;
     ring = 0;
     uint32_t o = (uint32_t)nws * slots * 1024;
-    // int4: parked k-tiles (K rounded up to whole rounds) and scales padded
-    // to whole 4-tile chunks
-    pp = pitch4(tpu * ks * upw);
+    // int4: parked k-tiles (K rounded up to whole rounds and to pairs of
+    // 4-tile chunks) and f32 scales padded to whole 4-tile chunks; group 64
+    // keeps its scales as f16 (ngh halves per row: whole 16-byte units, an
+    // odd number of them, so 16-byte reads by consecutive rows hit distinct
+    // banks) in the same area
+    pp = pitch4((tpu * ks * upw + 7) / 8 * 8);
     ngp = pitch4((kb + 3) / 4 * 4);
+    ngh = (kb + 7) / 8 * 8;
+    if (((ngh / 8) & 1) == 0) ngh += 8;
     park = o;
     o += (bits == 4 && !pir) ? (uint32_t)nbw * out * pp * 4 : 0;
     scl = o;
-    o += bits == 4 ? (uint32_t)nbw * 16 * ngp * 4 : 0;
+    o += bits == 4 ? (uint32_t)nbw * 16 * (ngp * 4 > ngh * 2 ? ngp * 4 : ngh * 2) : 0;
     asc = o;
     o += (uint32_t)(mp + 3) / 4 * 16;
     bsc = o;
@@ -183,9 +205,9 @@ struct Lay {
       const uint32_t ring_end = (uint32_t)nws * slots * 1024, need = ring_end + 3072 + 32;
       if (o < need) o = need;
     }
-    // the group-64 chain reads up to 2 CHP - 2 chunks of 16 bytes past the
-    // last scale row
-    if (bits == 4) o += 16 * (2 * CHP - 2);
+    // the group-64 chain reads up to 2 CHP - 2 pairs (32 bytes of sums, 16 of
+    // scales) past a row
+    if (bits == 4) o += 32 * (2 * CHP - 2);
     total = o;
   }
 };
@@ -308,14 +330,14 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
 #pragma unroll
   for (int mb = 0; mb < MB; mb++) acc[mb] = v4i{0, 0, 0, 0};
   const int npro = min(D - 1, UPWw);             // units issued before PRE
-  // group 64: the chain reads the parked sums four k-tiles at a time, up to
-  // k-tile 4 ceil(KB / 4); the stream parks TR * UPW of them (zeros past K).
+  // group 64: the chain reads the parked sums eight k-tiles at a time, up to
+  // k-tile 8 ceil(KB / 8); the stream parks TR * UPW of them (zeros past K).
   // When that is fewer (K of one or two k-tiles per round), the rest is set to
   // zero here -- LDS left by an earlier workgroup may hold any bits, a NaN
   // among them, and 0 * NaN would reach the output.  The barrier before the
   // chain orders these writes.
   if (BITS == 4 && G1 && !RAW && !PIR) {
-    const int lo = TR * UPW, hi = ((KB + 3) >> 2) * 4;
+    const int lo = TR * UPW, hi = ((KB + 7) >> 3) * 8;
     if (hi > lo) {
       float* Pz = (float*)(smem + L.park);
       for (int i = tid; i < NBW * OUT * (hi - lo); i += NT) {
@@ -405,17 +427,25 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   if (!RAW && tid < M) ASC[tid] = rscale;
 
   if (BITS == 4) {
-    // ---- q4g: group scales into LDS as f32 / 16, zero past the last group
-    // (padded k-tiles add +0); then one thread per output runs its chain
+    // ---- q4g: group scales into LDS, zero past the last group (padded
+    // k-tiles add +0): group 64 as the f16 bits (the chain's mixed fma takes
+    // them as they are), other group sizes as f32 / 16; then one thread per
+    // output runs its chain
     float* S = (float*)(smem + L.scl);
     if (!RAW) {
       const int per_g = 8 * NBW;
 #pragma unroll
       for (int v = 0; v < SPT; v++) {
         const int ii = tid + v * NT, gi = ii >> (3 + lnbw), c2 = ii - gi * per_g, qq = c2 >> 3;
-        if (gi < L.ngp && qq < NBW) {
+        const bool ok = gi < NG && qq < nb_here;
+        if (G1 && !PIR) {
+          if (gi < ((KB + 7) >> 3) * 8 && qq < NBW) {
+            uint16_t* d = (uint16_t*)S + (qq * 16 + 2 * (c2 & 7)) * L.ngh + gi;
+            d[0] = ok ? (uint16_t)(sreg[v] & 0xFFFF) : (uint16_t)0;
+            d[L.ngh] = ok ? (uint16_t)(sreg[v] >> 16) : (uint16_t)0;
+          }
+        } else if (gi < L.ngp && qq < NBW) {
           float* d = S + (qq * 16 + 2 * (c2 & 7)) * L.ngp + gi;
-          const bool ok = gi < NG && qq < nb_here;
           d[0] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] & 0xFFFF)) * 0.0625f : 0.0f;
           d[L.ngp] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] >> 16)) * 0.0625f : 0.0f;
         }
@@ -467,46 +497,56 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
         }
         a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
       } else if (G1 && !RAW) {
-        // group = k-tile: chunks of four, CHP - 1 chunks' sums and scales read
-        // ahead of the chunk being folded (the LDS round trip is longer than
-        // four dependent fmas; cfg2 pair 7.25 -> 7.2 us against 3 ahead).  The
-        // sums are parked as the floats the chain multiplies (converting them
-        // here instead put the conversion on the chain: 7.55 us).  LDS reads by address (ds_read_b128 in inline
-        // asm, waited for with lgkmcnt): the compiler would otherwise sink the
-        // prefetch next to its use.  Reads up to 2 CHP - 2 chunks past a row
-        // stay inside the workgroup's LDS (the layout's tail pad) and are not
-        // used.
+        // group = k-tile: pairs of 4-k-tile chunks, the sums of a pair in
+        // two 16-byte reads and its eight f16 scales in one (rows of the
+        // parked sums and of the scales are 16-byte aligned), CHP - 1 pairs
+        // read ahead of the pair being folded.  v_fma_mix_f32 takes the f16
+        // scale as it is (an exact widening, one rounding), so the chain runs
+        // on 16 acc and the unscaled s: every partial value is exactly 16
+        // times the reference's (never subnormal: nonzero sums of integer x f16
+        // products are at least 2^-24), and the 16 comes off exactly at the
+        // end.  LDS reads by address (inline asm, waited for with lgkmcnt):
+        // the compiler would otherwise sink the prefetch next to its use.
+        // Reads up to 2 CHP - 2 pairs past a row stay inside the workgroup's
+        // LDS (the layout's tail pad) and are not used.
         const uint32_t pa0 = lds0 + L.park + (uint32_t)((qq * OUT + oo) * L.pp) * 4u;
-        const uint32_t sa0 = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
-        const int nch = (KB + 3) >> 2;           // k-tiles past K hold zeros (parked or set above)
+        const uint32_t sa0 = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngh) * 2u;
+        const int npr = (KB + 7) >> 3;           // k-tiles past K hold zeros (parked or set above)
         float cacc = 0.0f;
-        v4i pv[CHP], sv[CHP];
+        v4i p0[CHP], p1[CHP], sv[CHP];
         sfor<0, CHP - 1>([&](auto bc) {
           constexpr int b = decltype(bc)::value;
-          lds_read2x128<16 * b>(pv[b], sv[b], pa0, sa0);
+          lds_read3x128<32 * b, 16 * b>(p0[b], p1[b], sv[b], pa0, sa0);
         });
-        // whole blocks of CHP chunks, then the last, partial block with a
-        // per-chunk test (outside the blocks the test would put a select on
+        // whole blocks of CHP pairs, then the last, partial block with a
+        // per-pair test (outside the blocks the test would put a select on
         // the fma chain's dependence path)
-        auto block = [&](int ch, auto partial) {
-          const uint32_t pb = pa0 + 16u * ch, sb = sa0 + 16u * ch;
+        auto block = [&](int pr, auto partial) {
+          const uint32_t pb = pa0 + 32u * pr, sb = sa0 + 16u * pr;
           sfor<0, CHP>([&](auto bc) {
-            constexpr int b = decltype(bc)::value;
-            lds_read2x128<16 * (b + CHP - 1)>(pv[(b + CHP - 1) % CHP], sv[(b + CHP - 1) % CHP], pb, sb);
-            lgkm_wait<2 * (CHP - 1)>(pv[b], sv[b]);
-            if (!decltype(partial)::value || ch + b < nch) {
-              cacc = __builtin_fmaf(__int_as_float(pv[b].x), __int_as_float(sv[b].x), cacc);
-              cacc = __builtin_fmaf(__int_as_float(pv[b].y), __int_as_float(sv[b].y), cacc);
-              cacc = __builtin_fmaf(__int_as_float(pv[b].z), __int_as_float(sv[b].z), cacc);
-              cacc = __builtin_fmaf(__int_as_float(pv[b].w), __int_as_float(sv[b].w), cacc);
+            constexpr int b = decltype(bc)::value, nb = (b + CHP - 1) % CHP;
+            lds_read3x128<32 * (b + CHP - 1), 16 * (b + CHP - 1)>(p0[nb], p1[nb], sv[nb], pb, sb);
+            lgkm_wait3<3 * (CHP - 1)>(p0[b], p1[b], sv[b]);
+            if (!decltype(partial)::value || pr + b < npr) {
+              cacc = __builtin_fmaf(__int_as_float(p0[b].x), f16lo(sv[b].x), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p0[b].y), f16hi(sv[b].x), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p0[b].z), f16lo(sv[b].y), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p0[b].w), f16hi(sv[b].y), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p1[b].x), f16lo(sv[b].z), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p1[b].y), f16hi(sv[b].z), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p1[b].z), f16lo(sv[b].w), cacc);
+              cacc = __builtin_fmaf(__int_as_float(p1[b].w), f16hi(sv[b].w), cacc);
             }
           });
         };
-        const int nfull = nch / CHP * CHP;
-        for (int ch = 0; ch < nfull; ch += CHP) block(ch, std::false_type{});
-        if (nfull < nch) block(nfull, std::true_type{});
-        sfor<0, CHP>([&](auto bc) { lgkm_wait<0>(pv[decltype(bc)::value], sv[decltype(bc)::value]); });
-        a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
+        const int nfull = npr / CHP * CHP;
+        for (int pr = 0; pr < nfull; pr += CHP) block(pr, std::false_type{});
+        if (nfull < npr) block(nfull, std::true_type{});
+        sfor<0, CHP>([&](auto bc) {
+          constexpr int b = decltype(bc)::value;
+          lgkm_wait3<0>(p0[b], p1[b], sv[b]);
+        });
+        a.C[(size_t)m * a.ldc + n] = (cacc * 0.0625f) * ASC[m];
       } else {
         // any group size, and the raw per-group sums
         float cacc = 0.0f;
@@ -581,7 +621,8 @@ bool fits_wg(int bits, int M, int K, int group, int nws, int ks, int nbw, bool p
   const Lay L = lay_for(bits, M, K, ks, nws, nbw, pir);
   if (bits == 4) {
     // the group-scale prefetch covers every padded group slot
-    if (8 * nbw * L.ngp > SPT * 64 * nws) return false;
+    const int slots_g = L.ngp > (K / 64 + 7) / 8 * 8 ? L.ngp : (K / 64 + 7) / 8 * 8;
+    if (8 * nbw * slots_g > SPT * 64 * nws) return false;
     (void)group;
   } else {
     // the q8c reduction reuses the rings
