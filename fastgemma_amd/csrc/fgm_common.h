@@ -104,20 +104,6 @@ FGM_DEV uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t 
   return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
-// buf_load_b128 issued as inline asm: the compiler neither sees nor waits
-// for it (its own waits count only the loads it sees, and around loads it
-// does not see they over-wait).  The caller waits with wait_vm and then
-// passes the registers through tie() before any use.
-FGM_DEV v4i buf_load_b128_nw(v4i rs, uint32_t voff, uint32_t soff) {
-  v4i r;
-  const int s0 = __builtin_amdgcn_readfirstlane((int)soff);
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(r) : "v"(voff), "s"(rs), "s"(s0) : "memory");
-  return r;
-}
-
-// Orders every later use of x after the (volatile) asm statements before it.
-FGM_DEV void tie(v4i& x) { asm volatile("" : "+v"(x)); }
-
 // threadIdx.x / 64 as a scalar: lets the compiler keep per-wave loop bounds
 // and tile indices in SGPRs and branch uniformly.
 FGM_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }

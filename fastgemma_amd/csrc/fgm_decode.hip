@@ -257,7 +257,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   const int UPWw = w < NWP ? UPW : 0;              // units this wave streams
   const v4i rb = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (live ? q : 0)) * KB * TB,
                             live ? (uint32_t)KB * TB : 0u);
-  const v4i ra = rsrc_words(a.A, (uint32_t)((M + 15) / 16) * KB * 1024);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, (uint32_t)((M + 15) / 16) * KB * 1024);
   const uint32_t bsw = BITS == 4 ? 16u * (uint32_t)(l ^ (((l >> 3) & 3) << 1))
                                  : 16u * (uint32_t)(l ^ (((l >> 4) & 3) << 2));
   uint32_t avoff[NA];
@@ -276,8 +276,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   const uint32_t ring_w = lds0 + L.ring + (uint32_t)w * L.slots * 1024;
 
   // one DMA of 1 KB of weights into ring slot sl, and the activation
-  // fragments of the same k-tiles into af[sl]; both waited for with wait_vm
-  // (X vector-memory instructions per unit, in issue order)
+  // fragments of the same k-tiles into af[sl]
   v4i af[D][NA];
   auto issue = [&](int u, auto slc) __attribute__((always_inline)) {
     constexpr int sl = decltype(slc)::value;
@@ -286,7 +285,7 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
     const uint32_t gu = PIR ? (uint32_t)(s * UPW + u) : (uint32_t)(u * KS + s);
     dma16<true>(rb, ring_w + sl * 1024, bsw, gu * 1024u);
 #pragma unroll
-    for (int x = 0; x < NA; x++) af[sl][x] = buf_load_b128_nw(ra, avoff[x], gu * TPU * 1024u);
+    for (int x = 0; x < NA; x++) af[sl][x] = buf_load_b128(ra, avoff[x], gu * TPU * 1024u);
   };
   // units 0 .. D - 2 in flight
   sfor<0, D - 1>([&](auto ic) {
@@ -367,8 +366,6 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
             if (later == k) wait_vm<k * X>();
           });
         }
-#pragma unroll
-        for (int x = 0; x < NA; x++) tie(af[i][x]);
         // B fragments of unit u
         const char* slot = smem + L.ring + ((size_t)w * L.slots + i) * 1024;
         v4i bv[TPU];
