@@ -463,38 +463,42 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
         // s UPW .. s UPW + UPW - 1 in its slots, so pair p (k-tiles 2p,
         // 2p + 1, 8 bytes per output) lies at 1 KB x p; its scales are floats
         // 2p, 2p + 1 of the column's row.  Groups of four pairs, read one
-        // group ahead (inline asm, waited for with lgkmcnt); reads past the
-        // last pair stay inside the workgroup's LDS and are not used.
-        const int np = (KB + 1) >> 1, ng = (np + 3) >> 2;
-        uint32_t pb = lds0 + L.ring + (uint32_t)(qq * KS * L.slots) * 1024u + (uint32_t)oo * 8u;
-        uint32_t sb = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
+        // group ahead (inline asm, waited for with lgkmcnt).  Every read and
+        // wait is unconditional -- the prefetch after the last group re-reads
+        // the last group, the pairs past the last one are skipped -- so no
+        // register of a read still in flight reaches a branch's join, where
+        // the compiler could copy it before it lands.
+        const int np = (KB + 1) >> 1, ng = (np + 3) >> 2, nfg = np >> 2;
+        const uint32_t pb = lds0 + L.ring + (uint32_t)(qq * KS * L.slots) * 1024u + (uint32_t)oo * 8u;
+        const uint32_t sb = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
         float cacc = 0.0f;
         v2i pv[2][4];
         v4i sv[2][2];
         pir_read(pv[0], sv[0], pb, sb);
-        for (int gi = 0; gi < ng; gi += 2) {
-          sfor<0, 2>([&](auto hc) {
-            constexpr int h = decltype(hc)::value;
-            if (gi + h < ng) {
-              if (gi + h + 1 < ng) {
-                pir_read(pv[h ^ 1], sv[h ^ 1], pb + 4096u * (h + 1), sb + 32u * (h + 1));
-                pir_wait6(pv[h], sv[h]);
-              } else {
-                pir_wait0(pv[h], sv[h]);
-              }
-              const int p0 = 4 * (gi + h);
+        // group gg from slot h (gg % 2), the next group into the other slot
+        auto fold = [&](int gg, auto hc, auto partial) {
+          constexpr int h = decltype(hc)::value;
+          const int gn = gg + 1 < ng ? gg + 1 : ng - 1;
+          pir_read(pv[h ^ 1], sv[h ^ 1], pb + 4096u * gn, sb + 32u * gn);
+          pir_wait6(pv[h], sv[h]);
 #pragma unroll
-              for (int b = 0; b < 4; b++)
-                if (p0 + b < np) {
-                  const int sx = sv[h][b >> 1][2 * (b & 1)], sy = sv[h][b >> 1][2 * (b & 1) + 1];
-                  cacc = __builtin_fmaf(__int_as_float(pv[h][b].x), __int_as_float(sx), cacc);
-                  cacc = __builtin_fmaf(__int_as_float(pv[h][b].y), __int_as_float(sy), cacc);
-                }
+          for (int b = 0; b < 4; b++)
+            if (!decltype(partial)::value || 4 * gg + b < np) {
+              const int sx = sv[h][b >> 1][2 * (b & 1)], sy = sv[h][b >> 1][2 * (b & 1) + 1];
+              cacc = __builtin_fmaf(__int_as_float(pv[h][b].x), __int_as_float(sx), cacc);
+              cacc = __builtin_fmaf(__int_as_float(pv[h][b].y), __int_as_float(sy), cacc);
             }
-          });
-          pb += 8192u;
-          sb += 64u;
+        };
+        int gg = 0;
+        for (; gg + 2 <= nfg; gg += 2) {
+          fold(gg, std::integral_constant<int, 0>{}, std::false_type{});
+          fold(gg + 1, std::integral_constant<int, 1>{}, std::false_type{});
         }
+        // the (at most two) groups left, either of them partial or past the end
+        fold(gg, std::integral_constant<int, 0>{}, std::true_type{});
+        fold(gg + 1, std::integral_constant<int, 1>{}, std::true_type{});
+        pir_wait0(pv[0], sv[0]);
+        pir_wait0(pv[1], sv[1]);
         a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
       } else if (G1 && !RAW) {
         // group = k-tile: pairs of 4-k-tile chunks, the sums of a pair in
