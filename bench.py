@@ -929,9 +929,10 @@ def _rec(t, work, unit):
 
 
 def cpu_configs(cp):
-    """Every BASELINE config on the CPU path, GEMM-only and prep + GEMM
-    on host-generated operands of the GPU rows'
-    shapes; the units and algorithmic work are the GPU rows'."""
+    """Every BASELINE config on the CPU path, GEMM-only and prep + GEMM (as
+    the reference's own kernel bench times them apart), on host-generated
+    operands of the GPU rows' shapes; the units and algorithmic work are the
+    GPU rows'."""
     import numpy as np
     rng = np.random.default_rng(99)
 

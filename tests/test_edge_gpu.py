@@ -77,7 +77,7 @@ def test_empty_contraction_writes_zeros_in_range_only(kind, M):
 @pytest.mark.parametrize("M,N,Kd", [(2048, 2048, 4160), (256, 2048, 576), (256, 2048, 1088), (256, 512, 8256)])
 def test_dense_odd_k_blocks(M, N, Kd):
     """K = 64 * odd: the K-group variants end on stages of zero-padded
-    k-blocks (ADVICE: K = 4160 takes the kmin >= 4096 path)."""
+    k-blocks (K = 4160 takes the kmin >= 4096 path)."""
     from fastgemma_amd import kernels as K
     print("q8c", M, N, Kd, K.gemm_path(8, M, Kd), flush=True)
     A = oracle.gen_i8(17 + Kd, M * Kd, -127, 127).reshape(M, Kd)
