@@ -593,6 +593,165 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
   }
 }
 
+// Park-in-ring grids whose waves stream four units per n-block (UPW = 4:
+// K = 2048, 4096, 8192 with 4, 8, 16 waves): each wave streams ITS k-slice
+// of TWO consecutive n-blocks, so one activation fragment serves two weight
+// units (a wave's fragments are as many bytes as its weights otherwise, and
+// they cost: the 134 MB stream ran 30.0 us with them, 26 us without).  A
+// workgroup: 2 n-blocks, KS waves; wave s holds units s * 4 .. s * 4 + 3 of
+// both in eight ring slots (n-block i's unit u in slot 4 i + u) and parks
+// each unit's sums in its slot, so n-block i's pair p = 4 s + u lies at
+// 1 KB x (8 s + 4 i + u): groups of four pairs (one wave's units) 8 KB
+// apart.  Per n-block the arithmetic is decode_kernel's park-in-ring path,
+// so the bytes are too.
+//
+// Vector-memory order of a wave: per unit u, n-block 0's and n-block 1's
+// weights and the unit's activation fragment (X2 = 3), all four units at
+// once; then PRE.  So unit u has landed when at most (3 - u) X2 + PRE remain.
+__global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
+  constexpr int OUT = 128, UPW = 4, X2 = 3, PRE = SPT + 1;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const GemmProb a = pick_problem(bt);
+  fetch_all(a);
+  if ((int)blockIdx.x >= a.nwg) return;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int w = wave_id(), l = tid & 63, g = l >> 4, j = l & 15;
+  const int M = a.M, N = a.N, KB = a.K >> 6;
+  const int KS = NT >> 6, NG = KB;
+  const Lay L(4, OUT, 2 * UPW, KS, 2 * UPW, KS, 2, KB, 8, true);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+  const int s = w;
+  int lb = (int)blockIdx.x;
+  const int nwgp = a.nwg;
+  if ((nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
+  const int nb_first = a.n0 + lb * 2;
+  const int nb_here = min(2, a.n0 + a.nblocks - nb_first);
+
+  // ---- the stream: both n-blocks' units and the activation fragments
+  const uint32_t bsw = 16u * (uint32_t)(l ^ (((l >> 3) & 3) << 1));
+  const v4i rb0 = rsrc_words((const int8_t*)a.B + (size_t)nb_first * KB * 512, (uint32_t)KB * 512);
+  const v4i rb1 = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (nb_here > 1 ? 1 : 0)) * KB * 512,
+                             nb_here > 1 ? (uint32_t)KB * 512 : 0u);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, (uint32_t)((M + 15) / 16) * KB * 1024);
+  const int r8 = j & 7;
+  const uint32_t avoff = r8 < M ? (uint32_t)((j >> 3) * 1024 + r8 * 64 + 16 * g) : FGM_OOB;
+  const uint32_t ring_w = lds0 + L.ring + (uint32_t)w * L.slots * 1024;
+  v4i af[UPW];
+#pragma unroll
+  for (int u = 0; u < UPW; u++) {
+    const uint32_t gu = (uint32_t)(s * UPW + u);
+    dma16<true>(rb0, ring_w + u * 1024, bsw, gu * 1024u);
+    dma16<true>(rb1, ring_w + (UPW + u) * 1024, bsw, gu * 1024u);
+    af[u] = buf_load_b128(ra, avoff, gu * 2048u);
+  }
+  // ---- PRE: group scales of both n-blocks, a_scale
+  uint32_t sreg[SPT];
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.b_scale, (uint32_t)NG * N * 2);
+  constexpr int per_g = 16;  // dwords per group: two n-blocks of 16 columns, two columns a dword
+#pragma unroll
+  for (int v = 0; v < SPT; v++) {
+    const int i = tid + v * NT, gi = i >> 4, c2 = i - gi * per_g, qq = c2 >> 3;
+    const bool ok = gi < NG && qq < nb_here;
+    sreg[v] = (uint32_t)buf_load_b32(rs, ok ? (uint32_t)((gi * N + (nb_first + qq) * 16 + 2 * (c2 & 7)) * 2) : FGM_OOB, 0);
+  }
+  const __amdgpu_buffer_rsrc_t ras = make_rsrc(a.a_scale, (uint32_t)M * 4);
+  const float rscale = __int_as_float(buf_load_b32(ras, tid < M ? (uint32_t)tid * 4 : FGM_OOB, 0));
+
+  uint32_t boff[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int c = (8 * g + 2 * t + ((j & 7) >> 2)) ^ (g << 1);
+    boff[t] = 16u * (uint32_t)c + 4u * (uint32_t)(j & 3);
+  }
+  const int sh = j < 8 ? 4 : 0;
+
+  sfor<0, UPW>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    wait_vm<(UPW - 1 - u) * X2 + PRE>();
+    const v4i x0 = af[u];
+    v4i x1;
+#pragma unroll
+    for (int d = 0; d < 4; d++) x1[d] = ror8(x0[d]);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      char* slot = smem + L.ring + ((size_t)w * L.slots + i * UPW + u) * 1024;
+      v4i bv[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const uint32_t x = *(const uint32_t*)(slot + e * 512 + boff[t]);
+          bv[e][t] = (int)((x << sh) & 0xF0F0F0F0u);
+        }
+      const v4i t0 = mfma16(x0, bv[0], v4i{0, 0, 0, 0});
+      const v4i t1 = mfma16(x1, bv[1], v4i{0, 0, 0, 0});
+      // park: the slot just read holds [output][k-tile of the unit]
+      float* Pr = (float*)slot;
+      if (g < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int oo = (4 * g + r) * 16 + j;
+          *(float2*)(Pr + 2 * oo) = float2{(float)t0[r], (float)t1[r]};
+        }
+      }
+    }
+  });
+  wait_vm<0>();  // the stream and PRE landed; no DMA still writes the ring
+
+  float* ASC = (float*)(smem + L.asc);
+  if (tid < M) ASC[tid] = rscale;
+  // group scales into LDS as f32 / 16 ([n-block][column][group], pitch ngp;
+  // zero past the last group)
+  float* S = (float*)(smem + L.scl);
+#pragma unroll
+  for (int v = 0; v < SPT; v++) {
+    const int ii = tid + v * NT, gi = ii >> 4, c2 = ii - gi * per_g, qq = c2 >> 3;
+    const bool ok = gi < NG && qq < nb_here;
+    if (gi < L.ngp && qq < 2) {
+      float* d = S + (qq * 16 + 2 * (c2 & 7)) * L.ngp + gi;
+      d[0] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] & 0xFFFF)) * 0.0625f : 0.0f;
+      d[L.ngp] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] >> 16)) * 0.0625f : 0.0f;
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < 2 * OUT; o += NT) {
+    const int qq = o / OUT, oo = o - qq * OUT, m = oo >> 4, c = oo & 15;
+    if (qq >= nb_here || m >= M) continue;
+    const int n = (nb_first + qq) * 16 + c;
+    // decode_kernel's park-in-ring chain with this layout's group stride
+    const int np = (KB + 1) >> 1, ng = (np + 3) >> 2, nfg = np >> 2;
+    const uint32_t pb = lds0 + L.ring + (uint32_t)(qq * UPW) * 1024u + (uint32_t)oo * 8u;
+    const uint32_t sb = lds0 + L.scl + (uint32_t)((qq * 16 + c) * L.ngp) * 4u;
+    float cacc = 0.0f;
+    v2i pv[2][4];
+    v4i sv[2][2];
+    pir_read(pv[0], sv[0], pb, sb);
+    auto fold = [&](int gg, auto hc, auto partial) {
+      constexpr int h = decltype(hc)::value;
+      const int gn = gg + 1 < ng ? gg + 1 : ng - 1;
+      pir_read(pv[h ^ 1], sv[h ^ 1], pb + 8192u * gn, sb + 32u * gn);
+      pir_wait6(pv[h], sv[h]);
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+        if (!decltype(partial)::value || 4 * gg + b < np) {
+          const int sx = sv[h][b >> 1][2 * (b & 1)], sy = sv[h][b >> 1][2 * (b & 1) + 1];
+          cacc = __builtin_fmaf(__int_as_float(pv[h][b].x), __int_as_float(sx), cacc);
+          cacc = __builtin_fmaf(__int_as_float(pv[h][b].y), __int_as_float(sy), cacc);
+        }
+    };
+    int gg = 0;
+    for (; gg + 2 <= nfg; gg += 2) {
+      fold(gg, std::integral_constant<int, 0>{}, std::false_type{});
+      fold(gg + 1, std::integral_constant<int, 1>{}, std::false_type{});
+    }
+    fold(gg, std::integral_constant<int, 0>{}, std::true_type{});
+    fold(gg + 1, std::integral_constant<int, 1>{}, std::true_type{});
+    pir_wait0(pv[0], sv[0]);
+    pir_wait0(pv[1], sv[1]);
+    a.C[(size_t)m * a.ldc + n] = cacc * ASC[m];
+  }
+}
+
 int pow2ceil(int x) {
   int p = 1;
   while (p < x) p *= 2;
@@ -759,6 +918,31 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   // up to the launch's NWS with idle n-blocks is not needed: every problem
   // uses NBW = NWS / KS unless its n-blocks run out
   const int NW = NWS;
+  // park in the ring with four units per wave and n-block and every problem
+  // split over all NW waves: two n-blocks per wave (decode_pir2_kernel)
+  if (pir) {
+    bool two = true;
+    for (int i = 0; i < bt.count; i++) two = two && bt.p[i].tw == 4 && bt.p[i].ks == NW;
+    if (two) {
+      GemmBatch b2 = bt;
+      int nwg2 = 0;
+      size_t lds2 = 0;
+      for (int i = 0; i < b2.count; i++) {
+        GemmProb& p = b2.p[i];
+        p.nbw = 2;
+        p.nwg = (p.nblocks + 1) / 2;
+        nwg2 = std::max(nwg2, p.nwg);
+        lds2 = std::max(lds2, (size_t)Lay(4, 128, 8, p.ks, 8, NW, 2, p.K / 64, 8, true).total);
+      }
+      if (lds2 <= 160 * 1024) {
+        static hipError_t attr = hipFuncSetAttribute((const void*)decode_pir2_kernel,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL(decode_pir2_kernel, dim3((nwg2 + 7) / 8 * 8, b2.count), dim3(NW * 64), lds2, st, b2);
+        return hipGetLastError();
+      }
+    }
+  }
   if (bits == 8) {
     if (half) return launch_decode<8, 1, true>(bt, g1, raw, false, NW, lds, nwg, st);
     switch (MB) {

@@ -81,7 +81,7 @@ def test_no_register_of_an_asm_lds_read_is_touched_before_its_wait(tmp_path):
     r = subprocess.run([HIPCC] + flags, cwd=CSRC, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-2000:]
     text = out.read_text()
-    parts = re.split(r"\n(_ZN\w*decode_kernel\w+):", text)
+    parts = re.split(r"\n(_ZN\w*decode_(?:pir2_)?kernel\w+):", text)
     assert len(parts) > 10, "no decode kernels found in the assembly"
     problems = {}
     for i in range(1, len(parts), 2):
