@@ -76,6 +76,9 @@ constexpr int CHP = 4;            // group-64 chain: pairs of 4-k-tile chunks in
 #ifndef FGM_DEC_PIR_MIN_WGS
 #define FGM_DEC_PIR_MIN_WGS 2048  // workgroups above which int4 sums are parked in the ring
 #endif
+#ifndef FGM_DEC_PIR2_MIN_WGS
+#define FGM_DEC_PIR2_MIN_WGS 2048 // above which, where the shapes allow, two n-blocks share a wave
+#endif
 
 // Two 16-byte LDS reads by byte address, and waits for all but the last six
 // LDS operations (or for all of them) that also order the use of the given
@@ -898,6 +901,10 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
     nwg_plain += (p.nblocks + NWS / p.ks - 1) / (NWS / p.ks);
   }
   pir = pir && nwg_plain > FGM_DEC_PIR_MIN_WGS;
+  // two n-blocks per wave (decode_pir2_kernel): int4 group 64, M <= 8, four
+  // units per wave and n-block, every problem split over all the waves
+  bool two = bits == 4 && half && g1 && !raw && nwg_plain > FGM_DEC_PIR2_MIN_WGS;
+  for (int i = 0; i < bt.count; i++) two = two && bt.p[i].tw == 4 && bt.p[i].ks == NWS;
   int nwg = 0;
   size_t lds = 0;
   for (int i = 0; i < bt.count; i++) {
@@ -918,29 +925,23 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
   // up to the launch's NWS with idle n-blocks is not needed: every problem
   // uses NBW = NWS / KS unless its n-blocks run out
   const int NW = NWS;
-  // park in the ring with four units per wave and n-block and every problem
-  // split over all NW waves: two n-blocks per wave (decode_pir2_kernel)
-  if (pir) {
-    bool two = true;
-    for (int i = 0; i < bt.count; i++) two = two && bt.p[i].tw == 4 && bt.p[i].ks == NW;
-    if (two) {
-      GemmBatch b2 = bt;
-      int nwg2 = 0;
-      size_t lds2 = 0;
-      for (int i = 0; i < b2.count; i++) {
-        GemmProb& p = b2.p[i];
-        p.nbw = 2;
-        p.nwg = (p.nblocks + 1) / 2;
-        nwg2 = std::max(nwg2, p.nwg);
-        lds2 = std::max(lds2, (size_t)Lay(4, 128, 8, p.ks, 8, NW, 2, p.K / 64, 8, true).total);
-      }
-      if (lds2 <= 160 * 1024) {
-        static hipError_t attr = hipFuncSetAttribute((const void*)decode_pir2_kernel,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (attr != hipSuccess) return attr;
-        hipLaunchKernelGGL(decode_pir2_kernel, dim3((nwg2 + 7) / 8 * 8, b2.count), dim3(NW * 64), lds2, st, b2);
-        return hipGetLastError();
-      }
+  if (two) {
+    GemmBatch b2 = bt;
+    int nwg2 = 0;
+    size_t lds2 = 0;
+    for (int i = 0; i < b2.count; i++) {
+      GemmProb& p = b2.p[i];
+      p.nbw = 2;
+      p.nwg = (p.nblocks + 1) / 2;
+      nwg2 = std::max(nwg2, p.nwg);
+      lds2 = std::max(lds2, (size_t)Lay(4, 128, 8, p.ks, 8, NW, 2, p.K / 64, 8, true).total);
+    }
+    if (lds2 <= 160 * 1024) {
+      static hipError_t attr = hipFuncSetAttribute((const void*)decode_pir2_kernel,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (attr != hipSuccess) return attr;
+      hipLaunchKernelGGL(decode_pir2_kernel, dim3((nwg2 + 7) / 8 * 8, b2.count), dim3(NW * 64), lds2, st, b2);
+      return hipGetLastError();
     }
   }
   if (bits == 8) {
