@@ -76,6 +76,9 @@ constexpr int CHP = 4;            // group-64 chain: pairs of 4-k-tile chunks in
 #ifndef FGM_DEC_PIR_MIN_WGS
 #define FGM_DEC_PIR_MIN_WGS 2048  // workgroups above which int4 sums are parked in the ring
 #endif
+#ifndef FGM_DEC_PIR_NPW
+#define FGM_DEC_PIR_NPW 2         // n-blocks per wave of the decode_pir2_kernel grids (2 or 4)
+#endif
 #ifndef FGM_DEC_PIR2_MIN_WGS
 #define FGM_DEC_PIR2_MIN_WGS 2048 // above which, where the shapes allow, two n-blocks share a wave
 #endif
@@ -611,8 +614,9 @@ __global__ __launch_bounds__(1024) void decode_kernel(GemmBatch bt) {
 // Vector-memory order of a wave: per unit u, n-block 0's and n-block 1's
 // weights and the unit's activation fragment (X2 = 3), all four units at
 // once; then PRE.  So unit u has landed when at most (3 - u) X2 + PRE remain.
+template <int NPW>
 __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
-  constexpr int OUT = 128, UPW = 4, X2 = 3, PRE = SPT + 1;
+  constexpr int OUT = 128, UPW = 4, X2 = NPW + 1, PRE = SPT + 1, LNPW = NPW == 4 ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmProb a = pick_problem(bt);
   fetch_all(a);
@@ -621,20 +625,22 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
   const int w = wave_id(), l = tid & 63, g = l >> 4, j = l & 15;
   const int M = a.M, N = a.N, KB = a.K >> 6;
   const int KS = NT >> 6, NG = KB;
-  const Lay L(4, OUT, 2 * UPW, KS, 2 * UPW, KS, 2, KB, 8, true);
+  const Lay L(4, OUT, NPW * UPW, KS, NPW * UPW, KS, NPW, KB, 8, true);
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   const int s = w;
   int lb = (int)blockIdx.x;
   const int nwgp = a.nwg;
   if ((nwgp & 7) == 0) lb = (lb & 7) * (nwgp >> 3) + (lb >> 3);
-  const int nb_first = a.n0 + lb * 2;
-  const int nb_here = min(2, a.n0 + a.nblocks - nb_first);
+  const int nb_first = a.n0 + lb * NPW;
+  const int nb_here = min(NPW, a.n0 + a.nblocks - nb_first);
 
   // ---- the stream: both n-blocks' units and the activation fragments
   const uint32_t bsw = 16u * (uint32_t)(l ^ (((l >> 3) & 3) << 1));
-  const v4i rb0 = rsrc_words((const int8_t*)a.B + (size_t)nb_first * KB * 512, (uint32_t)KB * 512);
-  const v4i rb1 = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (nb_here > 1 ? 1 : 0)) * KB * 512,
-                             nb_here > 1 ? (uint32_t)KB * 512 : 0u);
+  v4i rbs[NPW];
+#pragma unroll
+  for (int i = 0; i < NPW; i++)
+    rbs[i] = rsrc_words((const int8_t*)a.B + (size_t)(nb_first + (i < nb_here ? i : 0)) * KB * 512,
+                        i < nb_here ? (uint32_t)KB * 512 : 0u);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, (uint32_t)((M + 15) / 16) * KB * 1024);
   const int r8 = j & 7;
   const uint32_t avoff = r8 < M ? (uint32_t)((j >> 3) * 1024 + r8 * 64 + 16 * g) : FGM_OOB;
@@ -643,17 +649,17 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
 #pragma unroll
   for (int u = 0; u < UPW; u++) {
     const uint32_t gu = (uint32_t)(s * UPW + u);
-    dma16<true>(rb0, ring_w + u * 1024, bsw, gu * 1024u);
-    dma16<true>(rb1, ring_w + (UPW + u) * 1024, bsw, gu * 1024u);
+#pragma unroll
+    for (int i = 0; i < NPW; i++) dma16<true>(rbs[i], ring_w + (i * UPW + u) * 1024, bsw, gu * 1024u);
     af[u] = buf_load_b128(ra, avoff, gu * 2048u);
   }
   // ---- PRE: group scales of both n-blocks, a_scale
   uint32_t sreg[SPT];
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.b_scale, (uint32_t)NG * N * 2);
-  constexpr int per_g = 16;  // dwords per group: two n-blocks of 16 columns, two columns a dword
+  constexpr int per_g = 8 * NPW;  // dwords per group: NPW n-blocks of 16 columns, two columns a dword
 #pragma unroll
   for (int v = 0; v < SPT; v++) {
-    const int i = tid + v * NT, gi = i >> 4, c2 = i - gi * per_g, qq = c2 >> 3;
+    const int i = tid + v * NT, gi = i >> (3 + LNPW), c2 = i - gi * per_g, qq = c2 >> 3;
     const bool ok = gi < NG && qq < nb_here;
     sreg[v] = (uint32_t)buf_load_b32(rs, ok ? (uint32_t)((gi * N + (nb_first + qq) * 16 + 2 * (c2 & 7)) * 2) : FGM_OOB, 0);
   }
@@ -676,7 +682,7 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
 #pragma unroll
     for (int d = 0; d < 4; d++) x1[d] = ror8(x0[d]);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < NPW; i++) {
       char* slot = smem + L.ring + ((size_t)w * L.slots + i * UPW + u) * 1024;
       v4i bv[2];
 #pragma unroll
@@ -708,16 +714,16 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
   float* S = (float*)(smem + L.scl);
 #pragma unroll
   for (int v = 0; v < SPT; v++) {
-    const int ii = tid + v * NT, gi = ii >> 4, c2 = ii - gi * per_g, qq = c2 >> 3;
+    const int ii = tid + v * NT, gi = ii >> (3 + LNPW), c2 = ii - gi * per_g, qq = c2 >> 3;
     const bool ok = gi < NG && qq < nb_here;
-    if (gi < L.ngp && qq < 2) {
+    if (gi < L.ngp && qq < NPW) {
       float* d = S + (qq * 16 + 2 * (c2 & 7)) * L.ngp + gi;
       d[0] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] & 0xFFFF)) * 0.0625f : 0.0f;
       d[L.ngp] = ok ? f16_bits_to_f32((uint16_t)(sreg[v] >> 16)) * 0.0625f : 0.0f;
     }
   }
   __syncthreads();
-  for (int o = tid; o < 2 * OUT; o += NT) {
+  for (int o = tid; o < NPW * OUT; o += NT) {
     const int qq = o / OUT, oo = o - qq * OUT, m = oo >> 4, c = oo & 15;
     if (qq >= nb_here || m >= M) continue;
     const int n = (nb_first + qq) * 16 + c;
@@ -732,7 +738,7 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
     auto fold = [&](int gg, auto hc, auto partial) {
       constexpr int h = decltype(hc)::value;
       const int gn = gg + 1 < ng ? gg + 1 : ng - 1;
-      pir_read(pv[h ^ 1], sv[h ^ 1], pb + 8192u * gn, sb + 32u * gn);
+      pir_read(pv[h ^ 1], sv[h ^ 1], pb + 4096u * NPW * gn, sb + 32u * gn);
       pir_wait6(pv[h], sv[h]);
 #pragma unroll
       for (int b = 0; b < 4; b++)
@@ -929,18 +935,19 @@ hipError_t fgm_launch_decode(int bits, const GemmBatch& in, hipStream_t st) {
     GemmBatch b2 = bt;
     int nwg2 = 0;
     size_t lds2 = 0;
+    constexpr int NPW = FGM_DEC_PIR_NPW;
     for (int i = 0; i < b2.count; i++) {
       GemmProb& p = b2.p[i];
-      p.nbw = 2;
-      p.nwg = (p.nblocks + 1) / 2;
+      p.nbw = NPW;
+      p.nwg = (p.nblocks + NPW - 1) / NPW;
       nwg2 = std::max(nwg2, p.nwg);
-      lds2 = std::max(lds2, (size_t)Lay(4, 128, 8, p.ks, 8, NW, 2, p.K / 64, 8, true).total);
+      lds2 = std::max(lds2, (size_t)Lay(4, 128, 4 * NPW, p.ks, 4 * NPW, NW, NPW, p.K / 64, 8, true).total);
     }
     if (lds2 <= 160 * 1024) {
-      static hipError_t attr = hipFuncSetAttribute((const void*)decode_pir2_kernel,
+      static hipError_t attr = hipFuncSetAttribute((const void*)decode_pir2_kernel<NPW>,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
       if (attr != hipSuccess) return attr;
-      hipLaunchKernelGGL(decode_pir2_kernel, dim3((nwg2 + 7) / 8 * 8, b2.count), dim3(NW * 64), lds2, st, b2);
+      hipLaunchKernelGGL(decode_pir2_kernel<NPW>, dim3((nwg2 + 7) / 8 * 8, b2.count), dim3(NW * 64), lds2, st, b2);
       return hipGetLastError();
     }
   }
