@@ -77,6 +77,7 @@ struct Cfg {
   // time, once the stream is done
   static_assert(KW == 1 || (size_t)BM * BN * 4 <= TRASH, "K-group reduction space");
   static_assert(LDS <= 160 * 1024, "LDS per workgroup");
+  static_assert(BM % 64 == 0, "the epilogue's a_scale arrives in 64-row chunks");
 };
 
 template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT>
