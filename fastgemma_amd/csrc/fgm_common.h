@@ -86,6 +86,9 @@ FGM_DEV int8_t quant_tail(float v) {
 // how the kernels mask rows and columns without branches.
 constexpr int FGM_BUF_FLAGS = 0x00020000;  // gfx9 family descriptor word 3
 constexpr uint32_t FGM_OOB = 0x80000000u;  // an offset no buffer here reaches
+// Cache-policy operand of the buffer load / store builtins on gfx950: nt
+// (non-temporal, streamed past the caches' normal allocation).
+constexpr int FGM_CPOL_NT = 2;
 
 FGM_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
