@@ -80,7 +80,8 @@ struct Cfg {
   static_assert(BM % 64 == 0, "the epilogue's a_scale arrives in 64-row chunks");
 };
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT,
+          bool BNT = false>
 __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
       dma16(ra, alds[i] == SINK ? sink : sb + alds[i], live ? avoffs[i] : FGM_OOB, (uint32_t)kb * 1024);
 #pragma unroll
     for (int i = 0; i < UB; i++)
-      dma16(rb, blds[i] == SINK ? sink : sb + blds[i], live ? bvoffs[i] : FGM_OOB,
+      dma16<BNT>(rb, blds[i] == SINK ? sink : sb + blds[i], live ? bvoffs[i] : FGM_OOB,
             (uint32_t)kb * (BITS == 8 ? 1024 : 512));
     if (BITS == 4)
       dma16(rsc, w == 0 ? sb + C::A_BYTES + C::B_BYTES : sink, live ? svoff : FGM_OOB,
@@ -451,10 +452,11 @@ __global__ __launch_bounds__(64 * WGM * WGN * KW) void gemm_kernel(GemmBatch bt)
   }
 }
 
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW, bool RAW, bool G1, bool ROT,
+          bool BNT>
 hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
   using C = Cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW>;
-  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, RAW, G1, ROT>;
+  auto k = gemm_kernel<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, RAW, G1, ROT, BNT>;
   static hipError_t attr =
       hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
   if (attr != hipSuccess) return attr;
@@ -475,13 +477,13 @@ hipError_t launch_cfg(const GemmBatch& in, hipStream_t st) {
 
 // Variant: raw-accumulator dumps or scaled outputs; int4 with 64-wide groups
 // (a fresh accumulator every k-block) or the general group size.
-template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW = 1, bool ROT = false>
+template <int BITS, int WMT, int WNT, int WGM, int WGN, int NS, int KS, int KW = 1, bool ROT = false, bool BNT = false>
 hipError_t launch_any(const GemmBatch& b, hipStream_t st) {
-  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, true, false, ROT>(b, st);
+  if (b.p[0].acc_out) return launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, true, false, ROT, BNT>(b, st);
   bool g1 = BITS == 4;
   for (int i = 0; i < b.count; i++) g1 = g1 && b.p[i].group == 64;
-  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, BITS == 4, ROT>(b, st)
-            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false, ROT>(b, st);
+  return g1 ? launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, BITS == 4, ROT, BNT>(b, st)
+            : launch_cfg<BITS, WMT, WNT, WGM, WGN, NS, KS, KW, false, false, ROT, BNT>(b, st);
 }
 
 // Shortest K of a batch.
@@ -489,6 +491,13 @@ int kmin(const GemmBatch& b) {
   int k = b.p[0].K;
   for (int i = 1; i < b.count; i++) k = b.p[i].K < k ? b.p[i].K : k;
   return k;
+}
+
+// Most rows of a batch's problems.
+int mmax(const GemmBatch& b) {
+  int m = b.p[0].M;
+  for (int i = 1; i < b.count; i++) m = b.p[i].M > m ? b.p[i].M : m;
+  return m;
 }
 
 // Workgroup tiles of a batch for a BM x BN tile.
@@ -526,14 +535,25 @@ hipError_t fgm_launch_gemm(int bits, const GemmBatch& in, hipStream_t st) {
   // K groups of 16 waves, or the 128x64 tile on eight 32x32 waves, measured
   // slower (q 8.4, gate 12.9 us).
   if (bits == 8) {
+    // With at most 256 rows, two to four m-tiles share a weight tile and the
+    // weights are read with the non-temporal policy (M = 256, weights from
+    // HBM: q / o 6.85 -> 6.65 us, gate 10.2 -> 9.7 us, the 4-launch layer
+    // 50.3 -> 47.0 us); the down projection's k-rotated tiles (15.1 -> 15.8
+    // us) and every M = 2048 shape (down 38.7 -> 45.6 us: sixteen m-tiles
+    // share a weight tile there) keep the default policy.
+    const bool bnt = mmax(in) <= 256;
     if (tiles(in, 256, 128) >= 480) return launch_any<8, 4, 2, 2, 2, 2, 1>(in, st);
-    if (tiles(in, 128, 128) >= 240)  // long K (the down projection): two K groups
-      return kmin(in) >= 4096 ? launch_any<8, 2, 2, 2, 2, 4, 1, 2>(in, st)
-                              : launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
-    if (tiles(in, 128, 64) >= 240) return launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
-    if (tiles(in, 64, 64) >= 160) return launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
-    return kmin(in) >= 8192 ? launch_any<8, 1, 1, 2, 1, 4, 1, 4, true>(in, st)
-                            : launch_any<8, 1, 1, 2, 1, 4, 1, 4>(in, st);
+    if (tiles(in, 128, 128) >= 240) {  // long K (the down projection): two K groups
+      if (kmin(in) >= 4096) return launch_any<8, 2, 2, 2, 2, 4, 1, 2>(in, st);
+      return bnt ? launch_any<8, 2, 2, 2, 2, 4, 2, 1, false, true>(in, st)
+                 : launch_any<8, 2, 2, 2, 2, 4, 2>(in, st);
+    }
+    if (tiles(in, 128, 64) >= 240)
+      return bnt ? launch_any<8, 2, 1, 2, 2, 4, 2, 1, false, true>(in, st) : launch_any<8, 2, 1, 2, 2, 4, 2>(in, st);
+    if (tiles(in, 64, 64) >= 160)
+      return bnt ? launch_any<8, 1, 1, 2, 2, 3, 2, 2, false, true>(in, st) : launch_any<8, 1, 1, 2, 2, 3, 2, 2>(in, st);
+    if (kmin(in) >= 8192) return launch_any<8, 1, 1, 2, 1, 4, 1, 4, true>(in, st);
+    return bnt ? launch_any<8, 1, 1, 2, 1, 4, 1, 4, false, true>(in, st) : launch_any<8, 1, 1, 2, 1, 4, 1, 4>(in, st);
   }
   if (tiles(in, 128, 128) >= 480) return launch_any<4, 2, 2, 2, 2, 2, 2>(in, st);
   if (tiles(in, 128, 64) >= 240) return launch_any<4, 2, 1, 2, 2, 2, 2>(in, st);
