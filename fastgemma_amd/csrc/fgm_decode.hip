@@ -650,7 +650,10 @@ __global__ __launch_bounds__(1024) void decode_pir2_kernel(GemmBatch bt) {
   for (int u = 0; u < UPW; u++) {
     const uint32_t gu = (uint32_t)(s * UPW + u);
 #pragma unroll
-    for (int i = 0; i < NPW; i++) dma16<true>(rbs[i], ring_w + (i * UPW + u) * 1024, bsw, gu * 1024u);
+    // (the default cache policy: on these grids of many rounds of workgroups
+    // it streams better than the non-temporal one the one-round grids use,
+    // 134 MB stream 29.25 -> 28.05 us)
+    for (int i = 0; i < NPW; i++) dma16<false>(rbs[i], ring_w + (i * UPW + u) * 1024, bsw, gu * 1024u);
     af[u] = buf_load_b128(ra, avoff, gu * 2048u);
   }
   // ---- PRE: group scales of both n-blocks, a_scale
